@@ -1,0 +1,246 @@
+"""Benchmark of the INT4-G128-SYM projection path on one MI355X.
+
+Headline (one JSON line on stdout): BASELINE config 1 -- the decode MLP
+gate/up projection with the SiLU epilogue, M=1, K=5120, 2 x 17408 rows in
+one interleaved packed-INT4 matrix (W_up = W_gate + 17408*2560 bytes),
+17408 fp16 outputs.  One "step" = one launch over one batch.  The value is
+HBM GB/s of algorithmic bytes N*K/2 + N*(K/128)*2 + M*K*2 + M*N_out*2 per
+step divided by the wall time per step, with all inputs resident in HBM
+and the weights rotated over enough copies (> 512 MB) that the 256 MB
+Infinity Cache cannot hold them.
+
+The other BASELINE configs are measured the same way and reported under
+"suite" (disable with --quick).  The CPU baseline is the oracle restatement
+of the reference CPU loop, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0          # MI355X published HBM3E bandwidth
+FP16_PEAK_TFLOPS = 2500.0       # MI355X published dense FP16 MFMA
+MALL_BYTES = 256 << 20
+ROTATE_MIN_BYTES = 600 << 20
+
+
+def gemv_bytes(M, Nrows, K, Nout, out_bytes):
+    return Nrows * K // 2 + Nrows * (K // 128) * 2 + M * K * 2 + M * Nout * out_bytes
+
+
+def cpu_count():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+class Rig:
+    """Device buffers for one config: weight copies rotated per launch."""
+
+    def __init__(self, torch, dev, Nrows, K, sigma, seed=0):
+        from xinfer_amd import synth
+        self.torch = torch
+        W = synth.packed_weights(seed, Nrows, K)
+        S = synth.scales(seed, Nrows, K, sigma)
+        one = Nrows * K // 2 + Nrows * (K // 128) * 2
+        self.copies = max(2, -(-ROTATE_MIN_BYTES // one)) if one < 4 * MALL_BYTES else 2
+        w0 = torch.from_numpy(W).to(dev)
+        s0 = torch.from_numpy(S).view(torch.float16).to(dev)
+        self.W = [w0] + [w0.clone() for _ in range(self.copies - 1)]
+        self.S = [s0] + [s0.clone() for _ in range(self.copies - 1)]
+        self.host_W, self.host_S = W, S
+
+
+def time_launches(torch, launch, steps, warmup, copies):
+    for i in range(warmup):
+        launch(i % copies)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for i in range(steps):
+        launch(i % copies)
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall / steps, e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: this build's projection path is a "
+              "single-GPU kernel (multi-GPU sharding is design-only); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from xinfer_amd import ops, synth
+    from xinfer_amd._lib import load_library
+    load_library()
+    dev = torch.device("cuda:0")
+    log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
+
+    # ---------------- headline: config 1, fused gate/up + SiLU, M=1 ----------------
+    M, N, K = 1, 17408, 5120
+    rig = Rig(torch, dev, 2 * N, K, 0.02)
+    Xb = synth.activations(0, M, K)
+    X = torch.from_numpy(Xb).view(torch.float16).to(dev)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+    def launch_cfg1(i):
+        W, S = rig.W[i], rig.S[i]
+        ops.mlp_gate_up_swiglu_int4(Y, X, W[:N], S[:N], W[N:], S[N:], M, N, K)
+
+    copies = rig.copies
+    log(f"config 1: M={M} K={K} N=2x{N}, {copies} weight copies")
+    wall_step, ev_step = time_launches(torch, launch_cfg1, args.steps, args.warmup, rig.copies)
+    nbytes = gemv_bytes(M, 2 * N, K, N, 2)
+    value = nbytes / wall_step / 1e9
+    achieved = nbytes / ev_step / 1e9
+    log(f"  wall {wall_step*1e6:.2f} us/step, events {ev_step*1e6:.2f} us/launch, "
+        f"{achieved:.0f} GB/s")
+    del rig
+
+    suite = {}
+    if not args.quick:
+        suite = run_suite(torch, dev, ops, synth, args, log)
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(nbytes, log)
+
+    line = {
+        "metric": "INT4 GEMV HBM GB/s (% of MI355X peak) at M=1; prefill GEMM TFLOP/s at M=512",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_step * 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int4xf16->f32acc",
+        "data": "synthetic (SplitMix64 seed 0: uniform int4, |N(0,0.02)|/7 fp16 scales, N(0,1) fp16 x)",
+        "config": {"workload": "config1 fused gate/up SiLU decode GEMV", "M": M, "K": K,
+                   "N": f"2x{N}", "group_size": 128, "weight_copies_rotated": copies,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                     "traffic": None,
+                     "kernel": "gemv_int4_kernel<MR=1,R=4,EPI_SWIGLU>",
+                     "algorithmic_bytes_per_launch": nbytes,
+                     "avg_launch_us": round(ev_step * 1e6, 3)},
+        "cpu_baseline": cpu,
+        "suite": suite,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def run_suite(torch, dev, ops, synth, args, log):
+    out = {}
+    steps = max(20, min(args.steps, 200))
+    warm = min(args.warmup, 20)
+
+    def gemv_cfg(name, M, N, K, sigma=0.02):
+        rig = Rig(torch, dev, N, K, sigma)
+        X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+        Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        fn = lambda i: ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)  # noqa: E731
+        w, e = time_launches(torch, fn, steps, warm, rig.copies)
+        b = gemv_bytes(M, N, K, N, 2)
+        out[name] = {"M": M, "N": N, "K": K, "us": round(e * 1e6, 3), "GBps": round(b / e / 1e9, 1),
+                     "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"  {name}: {out[name]}")
+
+    gemv_cfg("northstar_gemv_m1_n34816_k5120", 1, 34816, 5120)
+    gemv_cfg("cfg0_qproj_m1_n6144_k5120", 1, 6144, 5120)
+    for m in (1, 2, 4, 8):
+        gemv_cfg(f"cfg2_down_m{m}_n5120_k17408", m, 5120, 17408)
+
+    # config 3: LM head + argmax (ids only, logits not stored)
+    N, K = 151936, 5120
+    rig = Rig(torch, dev, N, K, 0.01)
+    for M in (1, 8):
+        X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+        ids = torch.empty(M, dtype=torch.int32, device=dev)
+        scr = torch.empty(ops.lm_head_argmax_scratch_size(M, N, K), dtype=torch.uint8, device=dev)
+        fn = lambda i: ops.lm_head_argmax_int4(ids, None, X, rig.W[i], rig.S[i], M, N, K,  # noqa
+                                                scratch=scr)
+        w, e = time_launches(torch, fn, steps, warm, rig.copies)
+        b = gemv_bytes(M, N, K, 0, 0) + M * 4
+        out[f"cfg3_lmhead_argmax_m{M}"] = {"M": M, "N": N, "K": K, "us": round(e * 1e6, 3),
+                                           "GBps": round(b / e / 1e9, 1),
+                                           "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)}
+        log(f"  cfg3 M={M}: {out[f'cfg3_lmhead_argmax_m{M}']}")
+    del rig
+
+    # config 4: chunked-prefill GEMM M=512
+    M, N, K = 512, 17408, 5120
+    rig = Rig(torch, dev, N, K, 0.02)
+    X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+    fn = lambda i: ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)  # noqa: E731
+    w, e = time_launches(torch, fn, max(5, steps // 10), 3, rig.copies)
+    fl = 2 * M * N * K
+    out["cfg4_prefill_m512_n17408_k5120"] = {"us": round(e * 1e6, 2), "TFLOPs": round(fl / e / 1e12, 1),
+                                             "frac_fp16_mfma": round(fl / e / 1e12 / FP16_PEAK_TFLOPS, 4)}
+    log(f"  cfg4: {out['cfg4_prefill_m512_n17408_k5120']}")
+    return out
+
+
+def cpu_baseline(nbytes, log):
+    """Oracle restatement of the reference CPU loop (double accumulate), on
+    the full config-1 step, repeated for >= ~10 s per thread setting."""
+    try:
+        import oracle
+    except Exception as e:  # the oracle library travels prebuilt; report if it is absent
+        log(f"cpu baseline unavailable: {e}")
+        return None
+    from xinfer_amd import synth
+    M, N, K = 1, 17408, 5120
+    W = synth.packed_weights(0, 2 * N, K)
+    S = synth.scales(0, 2 * N, K)
+    X = oracle.f16_to_f32(synth.activations(0, M, K))
+    res = {}
+    for threads in (cpu_count(), 1):
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            oracle.swiglu_int4(X, W[:N], S[:N], W[N:], S[N:], M, N, K, nthreads=threads)
+            reps += 1
+            if time.perf_counter() - t0 >= 10.0:
+                break
+        dt = (time.perf_counter() - t0) / reps
+        res[threads] = (nbytes / dt / 1e9, dt, reps)
+        log(f"  cpu oracle {threads} thread(s): {dt*1e3:.1f} ms/step, {reps} reps")
+    cores = cpu_count()
+    v, dt, reps = res[cores]
+    return {"value": round(v, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"full config-1 step (M=1, K=5120, 2x17408 rows) x {reps} reps, "
+                      f"OpenMP over {cores} threads; single-thread: "
+                      f"{res[1][0]:.3f} GB/s ({res[1][1]*1e3:.0f} ms/step)",
+            "ms_per_step": round(dt * 1e3, 2)}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,328 @@
+"""GPU parity: the HIP kernels (through the C-ABI) against the CPU oracle on
+identical inputs.  Tolerances: the reference's own per-case bounds for its
+known-answer fixtures (tests/test_ops_oracle.cpp), and the BASELINE bound
+for fp16 outputs (max abs <= 1e-2, relative L2 <= 1e-3); argmax ids and
+dequantised weights bit-exact."""
+import glob
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests import kat
+from tests.gpu_util import check_f16_tol, cpu_threads, f16_dev, to_dev, to_np
+from xinfer_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xinfer_amd import _lib
+    _lib.load_library()
+    yield
+    torch.cuda.synchronize()
+
+
+def _ops():
+    from xinfer_amd import ops
+    return ops
+
+
+def _empty(shape, dtype):
+    import torch
+    return torch.full(shape, float("nan"), dtype=dtype, device="cuda")
+
+
+# ------------------------------------------- reference known-answer cases ----
+
+def test_golden_linear_fixtures():
+    import torch
+    ops = _ops()
+    for f in sorted(glob.glob(os.path.join(GOLDEN, "*.npz"))):
+        z = np.load(f, allow_pickle=False)
+        if str(z["kind"]) != "linear":
+            continue
+        M, N, K = (int(v) for v in z["shape"])
+        print("case", os.path.basename(f), flush=True)
+        W, S = to_dev(z["W"]), f16_dev(z["S"])
+        if bool(z["x_f16"]):
+            X = f16_dev(oracle.f32_to_f16(z["X"]))
+            Yh = _empty((M, N), torch.float16)
+            ops.linear_int4(Yh, X, W, S, None, M, N, K)
+            y = oracle.f16_to_f32(to_np(Yh))
+            assert np.abs(y - z["Y"]).max() <= 5e-3          # test_ops_oracle.cpp:768
+            Yf = _empty((M, N), torch.float32)
+            ops.linear_int4(Yf, X, W, S, None, M, N, K)
+            assert np.abs(to_np(Yf) - z["Y"]).max() <= 1e-4  # :781
+        Yf = _empty((M, N), torch.float32)
+        ops.linear_int4(Yf, to_dev(z["X"]), W, S, None, M, N, K)
+        tol = 1e-3 if N == 48 else 1e-4                        # :459 split-K, :356
+        assert np.abs(to_np(Yf) - z["Y"]).max() <= tol, f
+
+
+def test_reference_linear_m2_k5120_n2048_f32_and_naive():
+    import torch
+    ops = _ops()
+    M, N, K = 2, 2048, 5120                                   # test_ops_oracle.cpp:290-369
+    W = kat.pattern_weights(N, K, 3, 7)
+    S = kat.pattern_scales(N, K)
+    X = kat.uniform_x(46, M, K)
+    ref = oracle.linear_int4(X, W, S, M, N, K, nthreads=cpu_threads())
+    dW, dS, dX = to_dev(W), f16_dev(S), to_dev(X)
+    Y = _empty((M, N), torch.float32)
+    ops.linear_int4(Y, dX, dW, dS, None, M, N, K)
+    assert np.abs(to_np(Y) - ref).max() <= 1e-4
+    Y2 = _empty((M, N), torch.float32)
+    ops.linear_int4_naive(Y2, dX, dW, dS, None, M, N, K)
+    assert np.abs(to_np(Y2) - ref).max() <= 1e-4
+
+
+@pytest.mark.parametrize("xdtype", ["f32", "f16"])
+def test_reference_fused_four_projections(xdtype):
+    import torch
+    ops = _ops()
+    M, K, Ns = 1, 512, (128, 64, 48, 48)                      # test_ops_oracle.cpp:499-599
+    X = kat.uniform_x(49, M, K)
+    if xdtype == "f16":
+        X = oracle.f16_to_f32(oracle.f32_to_f16(X))
+        dX = f16_dev(oracle.f32_to_f16(X))
+        ydt = torch.float16
+    else:
+        dX = to_dev(X)
+        ydt = torch.float32
+    descs, refs, outs = [], [], []
+    for p, N in enumerate(Ns):
+        W = kat.pattern_weights(N, K, 3, 7, p)
+        S = kat.pattern_scales(N, K, p=p)
+        refs.append(oracle.linear_int4(X, W, S, M, N, K))
+        Y = _empty((M, N), ydt)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, N))
+    ops.linear_int4_fused(dX, descs, 4, M, K)
+    for Y, ref in zip(outs, refs):
+        if xdtype == "f16":
+            assert np.abs(oracle.f16_to_f32(to_np(Y)) - ref).max() <= 5e-3
+        else:
+            assert np.abs(to_np(Y) - ref).max() <= 1e-4
+
+
+@pytest.mark.parametrize("xdtype", ["f32", "f16"])
+def test_reference_swiglu(xdtype):
+    import torch
+    ops = _ops()
+    z = np.load(os.path.join(GOLDEN, "swiglu_m1_n256_k512.npz"), allow_pickle=False)
+    M, N, K = (int(v) for v in z["shape"])
+    X = z["X"]
+    if xdtype == "f16":
+        X = oracle.f16_to_f32(oracle.f32_to_f16(X))
+        ref = oracle.swiglu_int4(X, z["W"], z["S"], z["W2"], z["S2"], M, N, K)
+        Y = _empty((M, N), torch.float16)
+        ops.mlp_gate_up_swiglu_int4(Y, f16_dev(oracle.f32_to_f16(X)), to_dev(z["W"]),
+                                    f16_dev(z["S"]), to_dev(z["W2"]), f16_dev(z["S2"]), M, N, K)
+        assert np.abs(oracle.f16_to_f32(to_np(Y)) - ref).max() <= 5e-3
+    else:
+        Y = _empty((M, N), torch.float32)
+        ops.mlp_gate_up_swiglu_int4(Y, to_dev(X), to_dev(z["W"]), f16_dev(z["S"]),
+                                    to_dev(z["W2"]), f16_dev(z["S2"]), M, N, K)
+        assert np.abs(to_np(Y) - z["Y"]).max() <= 1e-4       # test_ops_oracle.cpp:695
+
+
+def test_reference_argmax_planted():
+    ops = _ops()
+    x = kat.uniform_x(48, 1, 248320, -100.0, 100.0)[0]       # test_ops_oracle.cpp:911-947
+    x[123456] = 999.0
+    assert ops.argmax(to_dev(x), 248320) == oracle.argmax(x) == 123456
+    z = np.load(os.path.join(GOLDEN, "argmax_v8192.npz"), allow_pickle=False)
+    assert ops.argmax(to_dev(z["X"]), 8192) == int(z["Y"])
+
+
+def test_dequant_bit_exact():
+    import torch
+    ops = _ops()
+    for (N, K) in ((16, 512), (6144, 5120)):
+        W = synth.packed_weights(0, N, K)
+        S = synth.scales(0, N, K)
+        out = _empty((N, K), torch.float32)
+        ops.dequant_int4(out, to_dev(W), f16_dev(S), N, K)
+        ref = oracle.dequant_int4(W, S, N, K)
+        assert np.array_equal(to_np(out).view(np.uint32), ref.view(np.uint32))
+
+
+# --------------------------------------------------- BASELINE configs ----
+
+def _linear_case(M, N, K, seed=0, sigma=0.02, out="f16", sample_rows=None):
+    import torch
+    ops = _ops()
+    W = synth.packed_weights(seed, N, K)
+    S = synth.scales(seed, N, K, sigma)
+    Xb = synth.activations(seed, M, K)
+    X = oracle.f16_to_f32(Xb)
+    ydt = torch.float16 if out == "f16" else torch.float32
+    Y = _empty((M, N), ydt)
+    ops.linear_int4(Y, f16_dev(Xb), to_dev(W), f16_dev(S), None, M, N, K)
+    y = to_np(Y)
+    rows = np.arange(M) if sample_rows is None else np.asarray(sample_rows)
+    ref = oracle.linear_int4(X[rows], W, S, len(rows), N, K, nthreads=cpu_threads())
+    y = y[rows]
+    if out == "f16":
+        return check_f16_tol(y, ref)
+    err = np.abs(y - ref).max()
+    assert err <= 1e-3 and kat.rel_l2(y, ref) <= 1e-5, err
+    return err, kat.rel_l2(y, ref)
+
+
+def test_cfg0_qproj_m1():
+    print(_linear_case(1, 6144, 5120))
+
+
+def test_north_star_gemv_m1_n34816():
+    print(_linear_case(1, 34816, 5120))
+
+
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
+def test_cfg2_down_proj_small_batch(M):
+    print(_linear_case(M, 5120, 17408))
+
+
+@pytest.mark.parametrize("M", [3, 5, 6, 7])
+def test_ragged_batch(M):
+    print(_linear_case(M, 1000, 1536, seed=M))
+
+
+@pytest.mark.parametrize("N,K", [(1, 128), (3, 384), (7, 640), (48, 5120), (129, 1152), (513, 3200)])
+def test_ragged_shapes_m1(N, K):
+    print(_linear_case(1, N, K, seed=N))
+    print(_linear_case(2, N, K, seed=N, out="f32"))
+
+
+def test_bias_is_added():
+    import torch
+    ops = _ops()
+    M, N, K = 2, 300, 1024
+    W, S = synth.packed_weights(5, N, K), synth.scales(5, N, K)
+    Xb = synth.activations(5, M, K)
+    bias = np.linspace(-2, 2, N).astype(np.float32)
+    Y = _empty((M, N), torch.float32)
+    ops.linear_int4(Y, f16_dev(Xb), to_dev(W), f16_dev(S), to_dev(bias), M, N, K)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, bias=bias)
+    assert np.abs(to_np(Y) - ref).max() <= 1e-4
+
+
+def test_cfg1_fused_gate_up_swiglu():
+    import torch
+    ops = _ops()
+    M, N, K = 1, 17408, 5120
+    # one interleaved allocation of 2N rows: W_up = W_gate + N*K/2
+    Wall = synth.packed_weights(0, 2 * N, K)
+    Sall = synth.scales(0, 2 * N, K)
+    Xb = synth.activations(0, M, K)
+    dW, dS = to_dev(Wall), f16_dev(Sall)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), dW[:N], dS[:N], dW[N:], dS[N:], M, N, K)
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb), Wall[:N], Sall[:N], Wall[N:], Sall[N:],
+                             M, N, K, nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y), ref))
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_cfg3_lm_head_argmax(M):
+    import torch
+    ops = _ops()
+    N, K = 151936, 5120
+    W, S = synth.packed_weights(0, N, K), synth.scales(0, N, K, 0.01)
+    Xb = synth.activations(0, M, K)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+    dX, dW, dS = f16_dev(Xb), to_dev(W), f16_dev(S)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    logits = _empty((M, N), torch.float32)
+    ops.lm_head_argmax_int4(ids, logits, dX, dW, dS, M, N, K)
+    got = to_np(ids)
+    lg = to_np(logits)
+    for m in range(M):
+        margin = oracle.top2_margin(ref[m])
+        print("row", m, "id", got[m], "margin", margin)
+        assert got[m] == oracle.argmax(ref[m])
+        assert got[m] == oracle.argmax(lg[m])
+    assert np.abs(lg - ref).max() <= 1e-3 and kat.rel_l2(lg, ref) <= 1e-5
+    # without storing logits, same ids; batched standalone argmax agrees
+    ids2 = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    ops.lm_head_argmax_int4(ids2, None, dX, dW, dS, M, N, K)
+    assert np.array_equal(to_np(ids2), got)
+    out64 = torch.full((M,), -1, dtype=torch.int64, device="cuda")
+    ops.argmax_rows(logits, out64, N, M)
+    assert np.array_equal(to_np(out64), got.astype(np.int64))
+
+
+def test_cfg4_prefill_m512_sampled_rows():
+    print(_linear_case(512, 17408, 5120, sample_rows=[0, 1, 77, 255, 256, 300, 510, 511]))
+
+
+# --------------------------------------------------------- argmax edges ----
+
+def test_argmax_edges():
+    import torch
+    ops = _ops()
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    cases = [
+        np.array([3, 7, 7, 1], np.float32),
+        np.array([nan, 5, 9], np.float32),
+        np.array([1, nan, 9, nan], np.float32),
+        np.array([-inf, -inf, -inf], np.float32),
+        np.array([-inf, nan, nan], np.float32),
+        np.array([nan, inf, 3], np.float32),
+        np.array([2.0], np.float32),
+    ]
+    big = kat.uniform_x(9, 1, 4096 * 3 + 17, -5, 5)[0]
+    big[4096 * 2 + 3] = 50.0
+    big[4096 + 1] = 50.0
+    cases.append(big)
+    for x in cases:
+        assert ops.argmax(to_dev(x), x.size) == oracle.argmax(x), x[:8]
+    # batched rows, V not a multiple of the block span
+    R, V = 5, 10007
+    xs = kat.uniform_x(10, R, V, -1, 1)
+    for r in range(R):
+        xs[r, (r * 997) % V] = 3.0
+    out = torch.full((R,), -1, dtype=torch.int64, device="cuda")
+    scratch = torch.empty(ops.argmax_scratch_size(V, R), dtype=torch.uint8, device="cuda")
+    ops.argmax_rows(to_dev(xs), out, V, R, scratch)
+    assert list(to_np(out)) == [oracle.argmax(xs[r]) for r in range(R)]
+    # empty vocab: token 0 (src/ops/sampling.cpp:17)
+    assert ops.argmax(to_dev(np.zeros(4, np.float32)), 0) == 0
+
+
+def test_lm_head_argmax_ties_lowest_index():
+    import torch
+    ops = _ops()
+    # duplicate rows in W give bit-identical logits: the lower row index must win
+    M, N, K = 1, 4096, 512
+    W, S = synth.packed_weights(2, N, K), synth.scales(2, N, K)
+    Xb = synth.activations(2, M, K)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K)
+    b = int(np.argmax(ref[0]))
+    for dst in (b + 1000) % N, (b + 3000) % N:
+        W[dst] = W[b]
+        S[dst] = S[b]
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    ops.lm_head_argmax_int4(ids, None, f16_dev(Xb), to_dev(W), f16_dev(S), M, N, K)
+    assert int(to_np(ids)[0]) == min(b, (b + 1000) % N, (b + 3000) % N)
+
+
+def test_noop_shapes_leave_output_untouched():
+    import torch
+    ops = _ops()
+    Y = torch.full((4,), 7.0, dtype=torch.float16, device="cuda")
+    X = torch.zeros(128, dtype=torch.float16, device="cuda")
+    W = torch.zeros(64, dtype=torch.uint8, device="cuda")
+    S = torch.zeros(1, dtype=torch.float16, device="cuda")
+    ops.linear_int4(Y, X, W, S, None, 0, 4, 128)
+    ops.linear_int4(Y, X, W, S, None, 1, 0, 128)
+    torch.cuda.synchronize()
+    assert (Y == 7.0).all()

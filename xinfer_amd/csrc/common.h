@@ -1,0 +1,106 @@
+// Shared device helpers for the gfx950 INT4-G128-SYM kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/xinfer_hip/xinfer_ops.h"
+
+namespace xhip {
+
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGroup = 128;  // k values per scale group (the only supported G)
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 v) { return __builtin_bit_cast(uint32_t, v); }
+__device__ __forceinline__ float h2f(uint16_t h) {
+    return (float)__builtin_bit_cast(f16, h);
+}
+
+// Dequantise one dword = 8 packed two's-complement nibbles (k0..k7, k0 in
+// bits 0-3) into four fp16 pairs holding exact integers in [-8, 7]:
+//   q[0] = (k0, k4), q[1] = (k1, k5), q[2] = (k2, k6), q[3] = (k3, k7).
+// Flipping bit 3 of a nibble turns two's complement into offset binary
+// u = q + 8; placing u (or 16u) in the mantissa of fp16 1024.0 gives exactly
+// 1024 + u (or 1024 + 16u).  Because the masked nibble bits never overlap the
+// exponent bits of 0x6400, "mask, flip bit 3, OR 0x6400" is one AND then one
+// XOR with 0x6408 (0x6480 for the high nibble): a single v_bitop3_b32.  One
+// packed add (or fma by 1/16) then removes the bias; all values are exact.
+__device__ __forceinline__ void dequant8(uint32_t w, f16x2 q[4]) {
+    const f16x2 kBias = {(f16)-1032.0f, (f16)-1032.0f};  // -(1024 + 8)
+    const f16x2 kSixteenth = {(f16)0.0625f, (f16)0.0625f};
+    const f16x2 kBias16 = {(f16)-72.0f, (f16)-72.0f};    // -(1024/16 + 8)
+    const uint32_t w8 = w >> 8;
+    q[0] = as_h2((w & 0x000F000Fu) ^ 0x64086408u) + kBias;
+    q[1] = as_h2((w & 0x00F000F0u) ^ 0x64806480u) * kSixteenth + kBias16;
+    q[2] = as_h2((w8 & 0x000F000Fu) ^ 0x64086408u) + kBias;
+    q[3] = as_h2((w8 & 0x00F000F0u) ^ 0x64806480u) * kSixteenth + kBias16;
+}
+
+// Rearrange 8 consecutive fp16 activations (x0..x7 held as 4 packed dwords,
+// natural order) into the pair order dequant8 produces.
+__device__ __forceinline__ void permute_x8(const uint32_t x[4], f16x2 p[4]) {
+    p[0] = as_h2(__builtin_amdgcn_perm(x[2], x[0], 0x05040100u));  // (x0, x4)
+    p[1] = as_h2(__builtin_amdgcn_perm(x[2], x[0], 0x07060302u));  // (x1, x5)
+    p[2] = as_h2(__builtin_amdgcn_perm(x[3], x[1], 0x05040100u));  // (x2, x6)
+    p[3] = as_h2(__builtin_amdgcn_perm(x[3], x[1], 0x07060302u));  // (x3, x7)
+}
+
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
+    return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// DPP / swizzle lane exchanges.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+        0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over each aligned group of 32 lanes; every lane receives the total.
+__device__ __forceinline__ float sum32(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]  (xor 1)
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]  (xor 2)
+    v += dpp<0x124>(v);  // row_ror:4
+    v += dpp<0x128>(v);  // row_ror:8  -> full 16-lane row sum
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(
+        __builtin_bit_cast(int, v), 0x401F));  // xor 16 within 32 lanes
+    return v;
+}
+
+// Argmax candidate ordering shared by every argmax kernel: larger value
+// wins, ties go to the lower index.  NaN handling reproduces a strict '>'
+// scan that starts from element 0: a NaN at index 0 is never beaten (mapped
+// to +inf, which also wins every tie by index), any other NaN never wins.
+struct ArgCand {
+    float v;
+    int32_t i;
+};
+
+__device__ __forceinline__ float argmax_key(float v, int64_t idx) {
+    if (v != v) return idx == 0 ? __builtin_inff() : -__builtin_inff();
+    return v;
+}
+
+__device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32_t bi) {
+    return av > bv || (av == bv && ai < bi);
+}
+
+}  // namespace xhip
+
+// Host-side helpers shared by the C-ABI translation units.
+namespace xhip_host {
+
+inline bool aligned(const void* p, uintptr_t a) {
+    return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+int num_cus();                 // compute units of the current device (cached)
+int launch_status();           // XINFER_OK or XINFER_ERR_HIP after a launch
+
+}  // namespace xhip_host
