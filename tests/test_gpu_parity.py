@@ -173,8 +173,9 @@ def _linear_case(M, N, K, seed=0, sigma=0.02, out="f16", sample_rows=None):
     y = y[rows]
     if out == "f16":
         return check_f16_tol(y, ref)
+    # fp32 outputs: the reference's fp16-in/fp32-out bound (test_ops_oracle.cpp:781)
     err = np.abs(y - ref).max()
-    assert err <= 1e-3 and kat.rel_l2(y, ref) <= 1e-5, err
+    assert err <= 1e-4 * max(1.0, np.abs(ref).max()) and kat.rel_l2(y, ref) <= 1e-4, err
     return err, kat.rel_l2(y, ref)
 
 
@@ -250,7 +251,8 @@ def test_cfg3_lm_head_argmax(M):
         print("row", m, "id", got[m], "margin", margin)
         assert got[m] == oracle.argmax(ref[m])
         assert got[m] == oracle.argmax(lg[m])
-    assert np.abs(lg - ref).max() <= 1e-3 and kat.rel_l2(lg, ref) <= 1e-5
+    assert np.abs(lg - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+    assert kat.rel_l2(lg, ref) <= 1e-4
     # without storing logits, same ids; batched standalone argmax agrees
     ids2 = torch.full((M,), -1, dtype=torch.int32, device="cuda")
     ops.lm_head_argmax_int4(ids2, None, dX, dW, dS, M, N, K)

@@ -58,12 +58,14 @@ _i32 = ctypes.c_int32
 _sz = ctypes.c_size_t
 
 
-def load_library(path: str = LIB_PATH):
+def load_library(path: str = None):
     """Load libxinfer_hip.so.  torch is imported first so the library binds to
     the HIP runtime torch already loaded (same soname)."""
     global _lib
     if _lib is not None:
         return _lib
+    # XINFER_HIP_LIB selects another build of the same library (tuning runs)
+    path = path or os.environ.get("XINFER_HIP_LIB") or LIB_PATH
     if not os.path.exists(path):
         raise RuntimeError(
             f"{path} is missing: build it with `python -m xinfer_amd.build` "

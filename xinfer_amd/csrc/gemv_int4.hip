@@ -3,20 +3,36 @@
 // Replaces the reference's sub-group GEMV family (src/ops/linear.cpp:33-163
 // split-K, 165-305 main, 351-498 fused, 501-617 SwiGLU) with one MI355X
 // design:
-//   * a "team" is 32 lanes (half a wave64).  A team owns R consecutive output
-//     rows at a time and walks K in steps of 1024: lane j reads the 16-byte
-//     chunk j of the step from each of its R rows (global_load_dwordx4, every
-//     half-wave instruction covers 512 contiguous bytes of one row).
-//   * the lane's 32 activations per m are loaded once per step and reused for
-//     all R rows; nibbles are dequantised in registers (dequant8) to exact
-//     fp16 integers and multiplied with v_dot2_f32_f16 (FP32 accumulate).
-//     The group scale is applied once per 32-k chunk in FP32.
-//   * the 4 waves (8 teams) of a block either take 8 different row sets or
-//     split K between 2/4/8 teams of the same row set (in-block split-K) so
-//     small-N shapes still fill 256 CUs; partials meet in LDS and are summed
-//     in a fixed order, so results are run-to-run deterministic.
-//   * the team's lanes are reduced with DPP row rotations + one ds_swizzle.
-// No MFMA: at M <= 8 the work is bound by HBM bandwidth of the weight stream.
+//   * a fixed grid of a few 256-thread blocks per CU; each block owns a
+//     contiguous range of output rows.  Its work is a list of items
+//     (group of 2R rows, 1024-k step) in row-major order, cut into 4 equal
+//     contiguous pieces, one per wave.  Small N therefore splits K across
+//     waves by itself (the reference's split-K).  Items are wave-uniform, so
+//     all item bookkeeping and row addresses live in SGPRs.
+//   * in an item, half-wave h covers rows 2R*g + h*R .. + R - 1; lane j of
+//     the half reads the 16-byte chunk j of the step from each row
+//     (global_load_dwordx4 with an SGPR base; a half-wave covers 512
+//     contiguous bytes of a row).  The next PF items are in flight while one
+//     is computed.
+//   * activations are staged once per block into LDS, permuted into the
+//     pair order of the nibble decode and stored piece-major (a half-wave's
+//     ds_read_b128 covers 512 contiguous bytes: no bank conflicts).
+//   * decode: "mask, flip bit 3, OR 0x6400" (one v_bitop3_b32 per nibble
+//     pair) turns nibble pairs into fp16 pairs (1024 + u, 1024 + u) or
+//     (1024 + 16u, 1024 + 16u) with u = q + 8, exactly.  These are fed straight
+//     to v_dot2_f32_f16 (FP32 accumulate) in two accumulators, and the bias is
+//     removed once per 32-k chunk:  sum_k x*q = ta + tb/16 - C, where
+//     C = 1032 * sum(x even k) + 72 * sum(x odd k) is precomputed per chunk
+//     during staging.  The group scale is applied to that chunk sum in FP32.
+//     When X does not fit in LDS the lanes read X from global memory and use
+//     the exact per-pair bias subtraction (dequant8) instead.
+//   * when a wave leaves a row group each half-wave reduces its 32 lanes (DPP
+//     row rotations + one ds_swizzle) and stores the partial in an LDS slot
+//     keyed by (row, first step of its run).  After a barrier the slots of
+//     each row are summed in step order: results do not depend on timing.
+// No MFMA: at M <= 8 the kernel is bound by the HBM weight stream.
+
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -32,7 +48,7 @@ struct GemvDesc {
     const float* bias;   // optional [N]
     void* Y;             // [M][N] output (EPI_ARGMAX: optional fp32 logits)
     int32_t N;
-    int32_t rowsets;     // ceil(N / R)
+    int32_t rows_blk;    // rows per block (multiple of 2R)
     int32_t block_begin; // first block of this descriptor
     int32_t pad;
 };
@@ -44,55 +60,175 @@ struct GemvParams {
     int32_t ndesc;
     int32_t M;           // real rows of X (<= MR)
     int32_t K;
-    int32_t ks;          // teams sharing one row set (1, 2, 4, 8)
+    int32_t pad;
 };
 
-constexpr int kTeams = 8;  // 32-lane teams per 256-thread block
+constexpr int kWaves = 4;  // waves per 256-thread block
 
-template <int MR, int R, int EPI, typename OutT>
+template <int RR>
+struct ItemRegs {
+    u32x4 w[RR];
+    uint32_t s[RR];  // raw fp16 scale bits: converted at use, so that a load
+                     // never forces a wait on the loads issued before it
+};
+
+// (1024 + u)-form decode of one dword: four fp16 pairs, u = q + 8.
+//   h[0] = (k0, k4) as 1024 + u     h[1] = (k1, k5) as 1024 + 16u
+//   h[2] = (k2, k6) as 1024 + u     h[3] = (k3, k7) as 1024 + 16u
+__device__ __forceinline__ void decode8_biased(uint32_t w, f16x2 h[4]) {
+    const uint32_t w8 = w >> 8;
+    h[0] = as_h2((w & 0x000F000Fu) ^ 0x64086408u);
+    h[1] = as_h2((w & 0x00F000F0u) ^ 0x64806480u);
+    h[2] = as_h2((w8 & 0x000F000Fu) ^ 0x64086408u);
+    h[3] = as_h2((w8 & 0x00F000F0u) ^ 0x64806480u);
+}
+
+// Two dwords at once: one 64-bit shift provides the ">> 8" of both
+// (bits 24-31 of the low result hold bits of the high dword, but only bits
+// 0-7 and 16-23 survive the masks).
+__device__ __forceinline__ void decode16_biased(uint32_t w0, uint32_t w1, f16x2 h[8]) {
+    const uint64_t w8 = (((uint64_t)w1 << 32) | w0) >> 8;
+    const uint32_t a8 = (uint32_t)w8, b8 = (uint32_t)(w8 >> 32);
+    h[0] = as_h2((w0 & 0x000F000Fu) ^ 0x64086408u);
+    h[1] = as_h2((w0 & 0x00F000F0u) ^ 0x64806480u);
+    h[2] = as_h2((a8 & 0x000F000Fu) ^ 0x64086408u);
+    h[3] = as_h2((a8 & 0x00F000F0u) ^ 0x64806480u);
+    h[4] = as_h2((w1 & 0x000F000Fu) ^ 0x64086408u);
+    h[5] = as_h2((w1 & 0x00F000F0u) ^ 0x64806480u);
+    h[6] = as_h2((b8 & 0x000F000Fu) ^ 0x64086408u);
+    h[7] = as_h2((b8 & 0x00F000F0u) ^ 0x64806480u);
+}
+
+template <int MR, int R, int EPI, typename OutT, bool XLDS, int PF>
 __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
-    constexpr int RR = (EPI == EPI_SWIGLU) ? 2 * R : R;  // weight rows per team
-    constexpr int NOUT = R * MR;
+    constexpr int RR = (EPI == EPI_SWIGLU) ? 2 * R : R;  // weight rows per half-wave item
+    constexpr int E = (EPI == EPI_SWIGLU) ? 2 : 1;       // sums per output
+    constexpr int G2 = 2 * R;                            // output rows per item
+
+    extern __shared__ __align__(16) unsigned char smem[];
 
     const int tid = threadIdx.x;
-    const int lane = tid & 31;
-    const int team = tid >> 5;
-    const int ks = p.ks;
-    const int rs_per_block = kTeams / ks;
-    const int rs_local = team / ks;
-    const int kslot = team - rs_local * ks;
+    const int lane = tid & 63;
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-    // descriptor of this block (blocks of one descriptor are contiguous)
     int di = 0;
 #pragma unroll
     for (int i = 1; i < 4; ++i)
         if (i < p.ndesc && (int)blockIdx.x >= p.d[i].block_begin) di = i;
     const GemvDesc& d = p.d[di];
-    const int rowset = ((int)blockIdx.x - d.block_begin) * rs_per_block + rs_local;
-    const bool active = rowset < d.rowsets;
     const int N = d.N;
     const int K = p.K;
-    const int n0 = rowset * R;
-    const int64_t row_bytes = K >> 1;
+    const int row_begin = ((int)blockIdx.x - d.block_begin) * d.rows_blk;
+    const int rows_here = min(d.rows_blk, N - row_begin);
+    const int groups = (rows_here + G2 - 1) / G2;
+    const uint32_t row_bytes = (uint32_t)K >> 1;
     const int ng = K >> 7;
     const int cpr = K >> 5;               // 16-byte chunks per row
     const int nsteps = (cpr + 31) >> 5;   // 1024-k steps
+    const int ragged = cpr & 31;          // chunks in a partial last step (0 = none)
 
-    const uint8_t* wrow[RR];
-    const uint16_t* srow[RR];
+    // LDS (XLDS): X pieces [step][m][piece v][lane] (u32x4) and the bias terms
+    // C [step][m][lane] (f32), padded to whole 1024-k steps; then partials.
+    // A half-wave's piece read covers 512 contiguous bytes (no bank conflicts)
+    // and the piece / m offsets are instruction immediates.
+    const int cpad = nsteps * 32;
+    u32x4* xs = reinterpret_cast<u32x4*>(smem);
+    float* xc = reinterpret_cast<float*>(smem + (size_t)(XLDS ? MR * 4 * cpad : 0) * 16);
+    float* part = xc + (XLDS ? MR * cpad : 0);
+    const int nslots = d.rows_blk * MR * E * nsteps;
+
+    const int items = groups * nsteps;
+    const int it0 = (wave * items) / kWaves;
+    const int it1 = ((wave + 1) * items) / kWaves;
+
+    const uint8_t* Wb0 = d.W;
+    const uint16_t* Sb0 = d.S;
+    const uint8_t* Wb1 = (EPI == EPI_SWIGLU) ? d.W2 : d.W;
+    const uint16_t* Sb1 = (EPI == EPI_SWIGLU) ? d.S2 : d.S;
+    const int row_last = row_begin + rows_here - 1;
+    // per-lane byte offsets inside an item (constant for the whole kernel)
+    const uint32_t w_lane = (uint32_t)(half * R) * row_bytes + (uint32_t)l32 * 16u;
+    const uint32_t s_lane = (uint32_t)(half * R * ng + (l32 >> 2)) * 2u;
+
+    // Raw buffer resources sized to the weight and scale matrices.  Every
+    // item issues the same loads with no branches (so the compiler keeps
+    // exact vmcnt bookkeeping across the prefetch ring): rows past N fall
+    // outside the resource and read as zero, and so do the lanes of a
+    // partial last k-step, whose offset is pushed out of range.  (Matrix
+    // sizes are checked on the host: < 4 GiB.)
+    const uint32_t srow_bytes = (uint32_t)ng * 2u;
+    const int nrec_w = (int)((uint32_t)N * row_bytes);
+    const int nrec_s = (int)((uint32_t)N * srow_bytes);
+    const __amdgpu_buffer_rsrc_t rw0 = __builtin_amdgcn_make_buffer_rsrc((void*)Wb0, (short)0, nrec_w, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc((void*)Wb1, (short)0, nrec_w, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)Sb0, (short)0, nrec_s, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc((void*)Sb1, (short)0, nrec_s, 0x00020000);
+    (void)row_last;
+
+    // load cursor (group, step) of the next item to fetch; wave-uniform.
+    // Items past the wave's range are fetched from an out-of-range offset:
+    // no memory traffic, zeros in the registers, zero contribution.
+    int lg = it0 / nsteps;
+    int ls = it0 - lg * nsteps;
+    int lcount = it1 - it0;
+
+    auto load_next = [&](ItemRegs<RR>& b) {
+        const uint32_t row0 = (uint32_t)(row_begin + lg * G2);   // first row of the item
+        const bool lane_bad = (ragged && ls == nsteps - 1 && l32 >= ragged) || lcount <= 0;
+        --lcount;
+        const uint32_t wv = lane_bad ? 0x80000000u : w_lane + row0 * row_bytes + (uint32_t)ls * 512u;
+        const uint32_t sv = lane_bad ? 0x80000000u : s_lane + row0 * srow_bytes + (uint32_t)ls * 16u;
 #pragma unroll
-    for (int r = 0; r < RR; ++r) {
-        const int rr = (EPI == EPI_SWIGLU) ? (r % R) : r;
-        int n = n0 + rr;
-        n = n < N ? n : N - 1;  // tail rows re-read the last row; never stored
-        const uint8_t* Wb = (EPI == EPI_SWIGLU && r >= R) ? d.W2 : d.W;
-        const uint16_t* Sb = (EPI == EPI_SWIGLU && r >= R) ? d.S2 : d.S;
-        wrow[r] = Wb + (int64_t)n * row_bytes;
-        srow[r] = Sb + (int64_t)n * ng;
+        for (int r = 0; r < RR; ++r) {
+            const int rr = (EPI == EPI_SWIGLU) ? (r % R) : r;
+            b.w[r] = __builtin_amdgcn_raw_buffer_load_b128(
+                (EPI == EPI_SWIGLU && r >= R) ? rw1 : rw0, (int)(wv + (uint32_t)rr * row_bytes), 0, 2 /*nt*/);
+        }
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            const int rr = (EPI == EPI_SWIGLU) ? (r % R) : r;
+            b.s[r] = __builtin_amdgcn_raw_buffer_load_b16(
+                (EPI == EPI_SWIGLU && r >= R) ? rs1 : rs0, (int)(sv + (uint32_t)rr * srow_bytes), 0, 0);
+        }
+        if (++ls == nsteps) { ls = 0; ++lg; }
+    };
+
+    ItemRegs<RR> buf[PF + 1];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) load_next(buf[j]);
+
+    // zero the partial slots; stage X (permuted) and the per-chunk bias terms
+    for (int i = tid; i < nslots; i += 256) part[i] = 0.0f;
+    if (XLDS) {
+        for (int i = tid; i < MR * cpad; i += 256) {
+            const int m = i / cpad;
+            const int c = i - m * cpad;
+            const int st = c >> 5, cl = c & 31;
+            const int mm = m < p.M ? m : p.M - 1;
+            float se = 0.0f, so = 0.0f;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                u32x4 xv = u32x4{0u, 0u, 0u, 0u};  // padding chunks read as x = 0
+                if (c < cpr) xv = *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3));
+                const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+                f16x2 pr[4];
+                permute_x8(xa, pr);
+                xs[((st * MR + m) * 4 + v) * 32 + cl] =
+                    u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f16x2 x2 = as_h2(xa[j]);
+                    se += (float)x2.x;
+                    so += (float)x2.y;
+                }
+            }
+            // sum_k x*q = ta + tb/16 - C with ta, tb the biased dot products
+            xc[(st * MR + m) * 32 + cl] = -(1032.0f * se + 72.0f * so);
+        }
     }
-    const f16* xrow[MR];
-#pragma unroll
-    for (int m = 0; m < MR; ++m) xrow[m] = p.X + (int64_t)(m < p.M ? m : p.M - 1) * K;
+    __syncthreads();
 
     float acc[RR][MR];
 #pragma unroll
@@ -100,122 +236,162 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
 
-    if (active) {
-        for (int step = kslot; step < nsteps; step += ks) {
-            const int c = (step << 5) + lane;
-            if (c < cpr) {
-                u32x4 wv[RR];
-                float sc[RR];
-#pragma unroll
-                for (int r = 0; r < RR; ++r)
-                    wv[r] = *reinterpret_cast<const u32x4*>(wrow[r] + (c << 4));
-#pragma unroll
-                for (int r = 0; r < RR; ++r) sc[r] = h2f(srow[r][c >> 2]);
-                f16x2 xp[MR][16];
-#pragma unroll
-                for (int m = 0; m < MR; ++m) {
-                    const u32x4* xs = reinterpret_cast<const u32x4*>(xrow[m] + (c << 5));
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) {
-                        u32x4 xv = xs[v];
-                        uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
-                        permute_x8(xa, &xp[m][4 * v]);
-                    }
-                }
-#pragma unroll
-                for (int r = 0; r < RR; ++r) {
-                    f16x2 q[16];
-                    dequant8(wv[r].x, &q[0]);
-                    dequant8(wv[r].y, &q[4]);
-                    dequant8(wv[r].z, &q[8]);
-                    dequant8(wv[r].w, &q[12]);
-#pragma unroll
-                    for (int m = 0; m < MR; ++m) {
-                        float t = 0.0f;
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) t = dot2(q[i], xp[m][i], t);
-                        acc[r][m] = __builtin_fmaf(t, sc[r], acc[r][m]);
-                    }
-                }
-            }
-        }
-    }
-
-    // reduce the 32 lanes of the team; every lane ends with every total
-#pragma unroll
-    for (int r = 0; r < RR; ++r)
-#pragma unroll
-        for (int m = 0; m < MR; ++m) acc[r][m] = sum32(acc[r][m]);
-
-    // in-block split-K: teams kslot>0 hand their totals to kslot 0 via LDS
-    __shared__ float red[kTeams][RR * MR];
-    if (ks > 1) {
-        if (lane == 0 && kslot > 0) {
-#pragma unroll
-            for (int r = 0; r < RR; ++r)
-#pragma unroll
-                for (int m = 0; m < MR; ++m) red[team][r * MR + m] = acc[r][m];
-        }
-        __syncthreads();
-        if (kslot == 0) {
-            for (int j = 1; j < ks; ++j) {
-#pragma unroll
-                for (int r = 0; r < RR; ++r)
-#pragma unroll
-                    for (int m = 0; m < MR; ++m) acc[r][m] += red[team + j][r * MR + m];
-            }
-        }
-    }
-
-    // lane l < R*MR of the kslot-0 team finalises output (r, m) = (l / MR, l % MR)
-    float val = 0.0f;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
+    auto compute_item = [&](int st, const ItemRegs<RR>& b) {
+        const int c = min((st << 5) + l32, cpr - 1);
+        f16x2 xp[MR][16];
+        float cm[MR];
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-            float v;
-            if (EPI == EPI_SWIGLU) {
-                const float g = acc[r][m];
-                const float u = acc[R + r][m];
-                v = g / (1.0f + expf(-g)) * u;
-            } else {
-                v = acc[r][m];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (XLDS) {
+                    const u32x4 xv = xs[((st * MR + m) * 4 + v) * 32 + l32];
+                    xp[m][4 * v + 0] = as_h2(xv.x);
+                    xp[m][4 * v + 1] = as_h2(xv.y);
+                    xp[m][4 * v + 2] = as_h2(xv.z);
+                    xp[m][4 * v + 3] = as_h2(xv.w);
+                } else {
+                    const int mm = m < p.M ? m : p.M - 1;
+                    const u32x4 xv = *reinterpret_cast<const u32x4*>(
+                        p.X + (size_t)mm * K + (c << 5) + (v << 3));
+                    const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+                    permute_x8(xa, &xp[m][4 * v]);
+                }
             }
-            if (lane == r * MR + m) val = v;
+            cm[m] = XLDS ? xc[(st * MR + m) * 32 + l32] : 0.0f;
+        }
+#pragma unroll
+        for (int r = 0; r < RR; ++r) {
+            if (XLDS) {
+                f16x2 h[16];
+                decode16_biased(b.w[r].x, b.w[r].y, &h[0]);
+                decode16_biased(b.w[r].z, b.w[r].w, &h[8]);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float ta = cm[m], tb = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 16; i += 2) {
+                        ta = dot2(h[i], xp[m][i], ta);
+                        tb = dot2(h[i + 1], xp[m][i + 1], tb);
+                    }
+                    acc[r][m] = __builtin_fmaf(__builtin_fmaf(tb, 0.0625f, ta), h2f((uint16_t)b.s[r]), acc[r][m]);
+                }
+            } else {
+                f16x2 q[16];
+                dequant8(b.w[r].x, &q[0]);
+                dequant8(b.w[r].y, &q[4]);
+                dequant8(b.w[r].z, &q[8]);
+                dequant8(b.w[r].w, &q[12]);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) t = dot2(q[i], xp[m][i], t);
+                    acc[r][m] = __builtin_fmaf(t, h2f((uint16_t)b.s[r]), acc[r][m]);
+                }
+            }
+        }
+    };
+
+    // store this wave's run of row group g (first step s0) and reset
+    auto flush = [&](int g, int s0) {
+#pragma unroll
+        for (int r = 0; r < RR; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[r][m] = sum32(acc[r][m]);
+        if (l32 == 0) {
+#pragma unroll
+            for (int r = 0; r < RR; ++r) {
+                const int rr = (EPI == EPI_SWIGLU) ? (r % R) : r;
+                const int e = (EPI == EPI_SWIGLU && r >= R) ? 1 : 0;
+                const int rl = g * G2 + half * R + rr;
+                if (rl < rows_here) {
+#pragma unroll
+                    for (int m = 0; m < MR; ++m)
+                        part[((rl * MR + m) * E + e) * nsteps + s0] = acc[r][m];
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < RR; ++r)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[r][m] = 0.0f;
+    };
+
+    // compute cursor (group, step); a run of one group starts at step run0.
+    // The ring loop has no branches around loads (exact vmcnt tracking); the
+    // item count is padded to a multiple of PF + 1 with zero items.
+    int cg = it0 / nsteps;
+    int cs = it0 - cg * nsteps;
+    int run0 = cs;
+    const int nreal = it1 - it0;
+    for (int base = 0; base < nreal; base += PF + 1) {
+#pragma unroll
+        for (int j = 0; j <= PF; ++j) {
+            const int k = base + j;
+            load_next(buf[(j + PF) % (PF + 1)]);
+            compute_item(min(cs, nsteps - 1), buf[j]);
+            if (k < nreal) {
+                if (++cs == nsteps || k + 1 == nreal) {
+                    flush(cg, run0);
+                    if (cs == nsteps) { cs = 0; ++cg; }
+                    run0 = cs;
+                }
+            }
         }
     }
-    const int orow = lane / MR;
-    const int om = lane - orow * MR;
-    const int n = n0 + orow;
-    const bool writer = active && kslot == 0 && lane < NOUT && n < N && om < p.M;
+    __syncthreads();
 
+    // epilogue: sum each output's slots in step order
+    const int nout = rows_here * MR;
     if (EPI == EPI_ARGMAX) {
-        __shared__ ArgCand cand[kTeams * NOUT];
-        if (writer && d.bias) val += d.bias[n];
-        if (writer && d.Y) reinterpret_cast<float*>(d.Y)[(int64_t)om * N + n] = val;
-        if (kslot == 0 && lane < NOUT) {
-            ArgCand c;
-            c.v = writer ? argmax_key(val, n) : -__builtin_inff();
-            c.i = writer ? n : 0x7FFFFFFF;
-            cand[rs_local * NOUT + lane] = c;
+        float bv = -__builtin_inff();
+        int32_t bi = 0x7FFFFFFF;
+        for (int o = tid; o < nout; o += 256) {
+            const int rl = o / MR, m = o - rl * MR;
+            float v = 0.0f;
+            for (int s = 0; s < nsteps; ++s) v += part[(rl * MR + m) * nsteps + s];
+            const int n = row_begin + rl;
+            if (d.bias) v += d.bias[n];
+            if (m < p.M) {
+                if (d.Y) reinterpret_cast<float*>(d.Y)[(size_t)m * N + n] = v;
+                const float key = argmax_key(v, n);
+                if (arg_better(key, n, bv, bi)) { bv = key; bi = n; }
+            }
         }
+        __syncthreads();  // partial slots are reused for the candidates below
+        float* cv = part;
+        int32_t* ci = reinterpret_cast<int32_t*>(part + 256);
+        cv[tid] = bv;
+        ci[tid] = bi;
         __syncthreads();
         if (tid < MR && tid < p.M) {
-            float bv = -__builtin_inff();
-            int32_t bi = 0x7FFFFFFF;
-            for (int t = 0; t < rs_per_block; ++t)
-                for (int r = 0; r < R; ++r) {
-                    const ArgCand c = cand[t * NOUT + r * MR + tid];
-                    if (arg_better(c.v, c.i, bv, bi)) { bv = c.v; bi = c.i; }
-                }
+            // thread t holds outputs with m == t % MR (256 is a multiple of MR)
+            float b = -__builtin_inff();
+            int32_t i = 0x7FFFFFFF;
+            for (int t = tid; t < 256; t += MR)
+                if (arg_better(cv[t], ci[t], b, i)) { b = cv[t]; i = ci[t]; }
             ArgCand o;
-            o.v = bv;
-            o.i = bi;
-            p.parts[(int64_t)tid * gridDim.x + blockIdx.x] = o;
+            o.v = b;
+            o.i = i;
+            p.parts[(size_t)tid * gridDim.x + blockIdx.x] = o;
         }
-    } else if (writer) {
-        if (EPI == EPI_PLAIN && d.bias) val += d.bias[n];
-        reinterpret_cast<OutT*>(d.Y)[(int64_t)om * N + n] = (OutT)val;
+    } else {
+        for (int o = tid; o < nout; o += 256) {
+            const int rl = o / MR, m = o - rl * MR;
+            if (m >= p.M) continue;
+            const int n = row_begin + rl;
+            float v = 0.0f;
+            for (int s = 0; s < nsteps; ++s) v += part[((rl * MR + m) * E) * nsteps + s];
+            if (EPI == EPI_SWIGLU) {
+                float u = 0.0f;
+                for (int s = 0; s < nsteps; ++s) u += part[((rl * MR + m) * E + 1) * nsteps + s];
+                v = v / (1.0f + expf(-v)) * u;
+            } else if (d.bias) {
+                v += d.bias[n];
+            }
+            reinterpret_cast<OutT*>(d.Y)[(size_t)m * N + n] = (OutT)v;
+        }
     }
 }
 
@@ -263,67 +439,160 @@ using namespace xhip;
 
 namespace {
 
-constexpr int kRowsM12 = 4;   // R for MR <= 2
-constexpr int kRowsM48 = 2;   // R for MR >= 4
 
 struct GemvPlan {
-    int mr, r, ks, blocks;
+    int mr, r, pf, blocks;
+    bool xlds;
+    size_t lds;
 };
 
-// Pick the in-block K split so the launch puts >= ~8 waves on every CU
-// (enough 16-byte loads in flight to cover HBM latency).
-int choose_ks(int64_t rowsets_total, int K) {
-    const int nsteps = (K / 32 + 31) / 32;
-    const int64_t target_waves = 8LL * xhip_host::num_cus();
-    int ks = 1;
-    while (ks < 8 && ks * 2 <= nsteps) {
-        const int64_t blocks = (rowsets_total + (kTeams / ks) - 1) / (kTeams / ks);
-        if (blocks * 4 >= target_waves) break;
-        ks *= 2;
+typedef void (*GemvKernel)(GemvParams);
+
+template <int MR, int R, int EPI, typename OutT, int PF>
+GemvKernel pick_kernel(bool xlds) {
+    return xlds ? gemv_int4_kernel<MR, R, EPI, OutT, true, PF>
+                : gemv_int4_kernel<MR, R, EPI, OutT, false, PF>;
+}
+
+template <int MR, int R, int EPI, typename OutT>
+GemvKernel pick_pf(bool xlds, int pf) {
+    if (MR == 1 && EPI != EPI_ARGMAX) {
+        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds);
+        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
+        return pick_kernel<MR, R, EPI, OutT, 3>(xlds);
     }
-    return ks;
+    return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
+}
+
+template <int EPI, typename OutT>
+GemvKernel kernel_for(int mr, int r, bool xlds, int pf) {
+    switch (mr) {
+        case 1:
+            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf)
+                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf) : pick_pf<1, 4, EPI, OutT>(xlds, pf);
+        case 2:
+            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf) : pick_pf<2, 4, EPI, OutT>(xlds, pf);
+        case 4:
+            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf) : pick_pf<4, 2, EPI, OutT>(xlds, pf);
+        default:
+            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf) : pick_pf<8, 2, EPI, OutT>(xlds, pf);
+    }
+}
+
+// Tuning overrides (read once): XINFER_GEMV_R, XINFER_GEMV_PF, XINFER_GEMV_BPC.
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+struct Overrides {
+    int r, pf, bpc;
+};
+const Overrides& overrides() {
+    static const Overrides o = {env_int("XINFER_GEMV_R", 0), env_int("XINFER_GEMV_PF", 0),
+                                env_int("XINFER_GEMV_BPC", 0)};
+    return o;
 }
 
 int mr_for(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
-template <int MR, int EPI, typename OutT>
-void launch_mr(GemvParams& p, int blocks, hipStream_t st) {
-    constexpr int R = MR <= 2 ? kRowsM12 : kRowsM48;
-    hipLaunchKernelGGL((gemv_int4_kernel<MR, R, EPI, OutT>), dim3(blocks), dim3(256), 0, st, p);
+// Resident blocks per CU for a kernel at a given dynamic LDS size (cached).
+int blocks_per_cu(GemvKernel k, size_t lds) {
+    struct Entry { GemvKernel k; size_t lds; int dev; int v; };
+    static Entry cache[256];
+    static int n = 0;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    for (int i = 0; i < n; ++i)
+        if (cache[i].k == k && cache[i].lds == lds && cache[i].dev == dev) return cache[i].v;
+    int v = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(k), 256, lds) !=
+            hipSuccess || v <= 0)
+        v = 1;
+    if (v > 8) v = 8;
+    if (n < 256) cache[n++] = Entry{k, lds, dev, v};
+    return v;
 }
 
+// Choose rows per item (R), rows per block and the grid.  Each block runs
+// ceil(rows_blk / R) * nsteps items over 8 teams; the estimated time is the
+// number of grid rounds times the busiest team's bytes (+ a per-item cost).
 template <int EPI, typename OutT>
-void launch_gemv(GemvParams& p, int blocks, int mr, hipStream_t st) {
-    switch (mr) {
-        case 1: launch_mr<1, EPI, OutT>(p, blocks, st); break;
-        case 2: launch_mr<2, EPI, OutT>(p, blocks, st); break;
-        case 4: launch_mr<4, EPI, OutT>(p, blocks, st); break;
-        default: launch_mr<8, EPI, OutT>(p, blocks, st); break;
-    }
-}
+GemvPlan plan_gemv(GemvParams& p, int mr) {
+    const int K = p.K;
+    const int cpr = K / 32;
+    const int nsteps = (cpr + 31) / 32;
+    const int E = EPI == EPI_SWIGLU ? 2 : 1;
+    const int cus = xhip_host::num_cus();
+    int64_t total_rows = 0;
+    for (int i = 0; i < p.ndesc; ++i) total_rows += p.d[i].N;
+    const size_t x_bytes = (size_t)mr * nsteps * 32 * (64 + 4);
+    const bool xlds = x_bytes + 4096 <= 64 * 1024;
 
-// Fill block ranges for the descriptors already stored in p.d[0..ndesc).
-int plan_blocks(GemvParams& p, int mr) {
-    const int R = mr <= 2 ? kRowsM12 : kRowsM48;
-    int64_t total_rs = 0;
-    for (int i = 0; i < p.ndesc; ++i) {
-        p.d[i].rowsets = (int32_t)((p.d[i].N + R - 1) / R);
-        total_rs += p.d[i].rowsets;
+    const int rcands[3] = {1, 2, 4};
+    const Overrides& ov = overrides();
+    const int pf = ov.pf > 0 ? ov.pf : 2;
+    GemvPlan best = {};
+    double best_cost = 1e300;
+    for (int ri = 0; ri < 3; ++ri) {
+        const int r = rcands[ri];
+        if ((mr == 2 && r == 1) || (mr >= 4 && r == 4)) continue;
+        if (ov.r > 0 && ov.r != r) continue;
+        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf);
+        // first guess of residency with a small partial area, then refine once
+        size_t lds = (xlds ? x_bytes : 0) + 4096;
+        int bpc = ov.bpc > 0 ? ov.bpc : blocks_per_cu(k, lds);
+        for (int pass = 0; pass < 2; ++pass) {
+            const int64_t target = (int64_t)cus * bpc;
+            int64_t rows_blk = (total_rows + target - 1) / target;
+            rows_blk = ((rows_blk + 2 * r - 1) / (2 * r)) * (2 * r);
+            if (rows_blk < 2 * r) rows_blk = 2 * r;
+            size_t part = (size_t)rows_blk * mr * E * nsteps * 4;
+            if (EPI == EPI_ARGMAX && part < 2048) part = 2048;
+            lds = (xlds ? x_bytes : 0) + part;
+            if (lds > 64 * 1024) { lds = 0; break; }  // not placeable: skip this R
+            const int bpc2 = ov.bpc > 0 ? ov.bpc : blocks_per_cu(k, lds);
+            if (pass == 0 && bpc2 != bpc) { bpc = bpc2; continue; }
+            int64_t blocks = 0;
+            for (int i = 0; i < p.ndesc; ++i) blocks += (p.d[i].N + rows_blk - 1) / rows_blk;
+            const int64_t rounds = (blocks + (int64_t)cus * bpc2 - 1) / ((int64_t)cus * bpc2);
+            const int64_t items = (rows_blk / (2 * r)) * nsteps;
+            const int64_t per_wave = (items + 3) / 4;
+            const double cost = (double)rounds * per_wave * (2 * r + 1.5);
+            if (cost < best_cost * 0.98 || (cost <= best_cost * 1.02 && r > best.r)) {
+                best_cost = cost;
+                best.mr = mr;
+                best.r = r;
+                best.xlds = xlds;
+                best.lds = lds;
+                best.pf = pf;
+                best.blocks = (int)blocks;
+                for (int i = 0; i < p.ndesc; ++i) p.d[i].rows_blk = (int32_t)rows_blk;
+            }
+            break;
+        }
     }
-    p.ks = choose_ks(total_rs, p.K);
-    const int rs_per_block = kTeams / p.ks;
+    // assign block ranges with the winning rows_blk
     int blocks = 0;
     for (int i = 0; i < p.ndesc; ++i) {
         p.d[i].block_begin = blocks;
-        blocks += (p.d[i].rowsets + rs_per_block - 1) / rs_per_block;
+        blocks += (p.d[i].N + p.d[i].rows_blk - 1) / p.d[i].rows_blk;
     }
     for (int i = p.ndesc; i < 4; ++i) p.d[i] = p.d[0], p.d[i].block_begin = 0x7FFFFFFF;
-    return blocks;
+    best.blocks = blocks;
+    return best;
+}
+
+template <int EPI, typename OutT>
+void launch_plan(const GemvParams& p, const GemvPlan& pl, hipStream_t st) {
+    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf);
+    hipLaunchKernelGGL(k, dim3(pl.blocks), dim3(256), pl.lds, st, p);
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int32_t G) {
     if (G != kGroup || (K % kGroup) != 0) return XINFER_ERR_UNSUPPORTED;
-    if (K > (1LL << 30) || N > (1LL << 30) || M > (1LL << 30)) return XINFER_ERR_UNSUPPORTED;
+    if (K > (1LL << 24) || N > (1LL << 30) || M > (1LL << 30)) return XINFER_ERR_UNSUPPORTED;
+    // the kernels address one weight matrix with 32-bit buffer offsets
+    if (N * (K / 2) >= (1LL << 32) - 4096) return XINFER_ERR_UNSUPPORTED;
     return XINFER_OK;
 }
 
@@ -346,16 +615,14 @@ int num_cus() {
 
 int launch_status() { return hipGetLastError() == hipSuccess ? XINFER_OK : XINFER_ERR_HIP; }
 
-// Shared by the C-ABI entry points and the MFMA GEMM fallback split:
-// runs the GEMV for one slab of at most 8 activation rows.
+// GEMV for one slab of at most 8 activation rows.
 template <int EPI, typename OutT>
 int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
     GemvParams p = base;
     p.M = (int32_t)M;
-    const int mr = mr_for(M);
-    const int blocks = plan_blocks(p, mr);
-    if (blocks <= 0) return XINFER_OK;
-    launch_gemv<EPI, OutT>(p, blocks, mr, st);
+    const GemvPlan pl = plan_gemv<EPI, OutT>(p, mr_for(M));
+    if (pl.blocks <= 0) return XINFER_OK;
+    launch_plan<EPI, OutT>(p, pl, st);
     return launch_status();
 }
 
@@ -485,8 +752,8 @@ size_t xinfer_lm_head_argmax_scratch_bytes(int64_t M, int64_t N, int64_t K) {
     p.ndesc = 1;
     p.K = (int32_t)(K > 0 ? K : 128);
     p.d[0].N = (int32_t)N;
-    const int blocks = plan_blocks(p, mr_for(M));
-    return (size_t)M * (size_t)blocks * sizeof(ArgCand);
+    const GemvPlan pl = plan_gemv<EPI_ARGMAX, float>(p, mr_for(M));
+    return (size_t)M * (size_t)pl.blocks * sizeof(ArgCand);
 }
 
 }  // extern "C"
@@ -519,8 +786,8 @@ extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* log
     p.d[0].S = reinterpret_cast<const uint16_t*>(scales);
     p.d[0].Y = logits;
     p.d[0].N = (int32_t)N;
-    const int mr = mr_for(M);
-    const int blocks = plan_blocks(p, mr);
+    const GemvPlan pl = plan_gemv<EPI_ARGMAX, float>(p, mr_for(M));
+    const int blocks = pl.blocks;
     const size_t need = (size_t)M * (size_t)blocks * sizeof(ArgCand);
     if (!scratch) {
         scratch = library_scratch(need);
@@ -529,7 +796,7 @@ extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* log
         return XINFER_ERR_SCRATCH;
     }
     p.parts = reinterpret_cast<ArgCand*>(scratch);
-    launch_gemv<EPI_ARGMAX, float>(p, blocks, mr, st);
+    launch_plan<EPI_ARGMAX, float>(p, pl, st);
     if (launch_status()) return XINFER_ERR_HIP;
     hipLaunchKernelGGL((argmax_finalize_kernel<int32_t>), dim3((unsigned)M), dim3(256), 0, st,
                        p.parts, (int32_t)blocks, ids);
