@@ -61,7 +61,13 @@ class Rig:
         self.host_W, self.host_S = W, S
 
 
-def time_launches(torch, launch, steps, warmup, copies):
+def time_launches(torch, launch, steps, warmup, copies, graph=False):
+    """Time `steps` launches rotating over `copies` weight copies.  Returns
+    (wall seconds per step, event seconds per step).  graph=True captures one
+    rotation of launches into a HIP graph (the way a decode step is replayed)
+    and times replays, which removes host launch overhead."""
+    if graph:
+        return _time_graph(torch, launch, steps, warmup, copies)
     for i in range(warmup):
         launch(i % copies)
     torch.cuda.synchronize()
@@ -75,6 +81,34 @@ def time_launches(torch, launch, steps, warmup, copies):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     return wall / steps, e0.elapsed_time(e1) * 1e-3 / steps
+
+
+def _time_graph(torch, launch, steps, warmup, copies):
+    per = copies * max(1, 32 // copies)          # launches per graph
+    for i in range(per):
+        launch(i % copies)                          # warm up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(per):
+                launch(i % copies)
+    reps = max(1, steps // per)
+    for _ in range(max(1, warmup // per)):
+        g.replay()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(reps):
+        g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    n = reps * per
+    return wall / n, e0.elapsed_time(e1) * 1e-3 / n
 
 
 def main():

@@ -328,3 +328,60 @@ def test_noop_shapes_leave_output_untouched():
     ops.linear_int4(Y, X, W, S, None, 1, 0, 128)
     torch.cuda.synchronize()
     assert (Y == 7.0).all()
+
+
+# ------------------------------------------------ prefill GEMM (M > 8) ----
+
+@pytest.mark.parametrize("M,N,K", [(9, 64, 128), (128, 272, 1024), (130, 300, 384), (512, 1000, 1024),
+                                   (256, 4352, 2048), (33, 17, 3072), (1000, 64, 1024)])
+def test_prefill_gemm_shapes(M, N, K):
+    print(_linear_case(M, N, K, seed=M + N))
+
+
+def test_prefill_gemm_f32_out_and_bias():
+    import torch
+    ops = _ops()
+    M, N, K = 200, 520, 2048
+    W, S = synth.packed_weights(8, N, K), synth.scales(8, N, K)
+    Xb = synth.activations(8, M, K)
+    bias = np.linspace(-1, 1, N).astype(np.float32)
+    Y = _empty((M, N), torch.float32)
+    ops.linear_int4(Y, f16_dev(Xb), to_dev(W), f16_dev(S), to_dev(bias), M, N, K)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, bias=bias, nthreads=cpu_threads())
+    err = np.abs(to_np(Y) - ref).max()
+    # q*s is rounded to fp16 on the MFMA path: bound it like the fp16 outputs
+    assert err <= 1e-2 and kat.rel_l2(to_np(Y), ref) <= 1e-3, err
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 256, 512), (40, 200, 1024), (512, 17408 // 8, 5120)])
+def test_prefill_swiglu(M, N, K):
+    import torch
+    ops = _ops()
+    Wg, Wu = synth.packed_weights(1, N, K), synth.packed_weights(1, N, K, synth.STREAM_W2)
+    Sg, Su = synth.scales(1, N, K), synth.scales(1, N, K, stream=synth.STREAM_S2)
+    Xb = synth.activations(1, M, K)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), to_dev(Wg), f16_dev(Sg), to_dev(Wu), f16_dev(Su),
+                                M, N, K)
+    rows = np.arange(0, M, max(1, M // 16))
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb)[rows], Wg, Sg, Wu, Su, len(rows), N, K,
+                             nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y)[rows], ref))
+
+
+def test_prefill_fused_descs_m64():
+    import torch
+    ops = _ops()
+    M, K, Ns = 64, 2048, (384, 128, 64)
+    Xb = synth.activations(4, M, K)
+    X = oracle.f16_to_f32(Xb)
+    descs, refs, outs = [], [], []
+    for p, N in enumerate(Ns):
+        W, S = synth.packed_weights(10 + p, N, K), synth.scales(10 + p, N, K)
+        refs.append(oracle.linear_int4(X, W, S, M, N, K))
+        Y = _empty((M, N), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, N))
+    ops.linear_int4_fused(f16_dev(Xb), descs, 3, M, K)
+    for Y, ref in zip(outs, refs):
+        check_f16_tol(to_np(Y), ref)

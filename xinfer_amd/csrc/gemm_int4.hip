@@ -1,14 +1,417 @@
-// INT4-G128-SYM projection for M > 8 (chunked prefill).  Placeholder that
-// runs the GEMV kernels on slabs of 8 activation rows until the MFMA GEMM
-// lands.
+// INT4-G128-SYM projection for M > 8 (chunked prefill) on gfx950: MFMA GEMM.
+//
+// The reference has no GEMM for this path: chunked prefill runs its GEMV
+// kernel with M = chunk (src/targets/qwen3_8/forward.cpp:284-287), which
+// re-streams every weight row once per activation row.  This kernel keeps
+// the same contract (the linear_int4 / mlp_gate_up_swiglu_int4 call at
+// M > 8) and computes it as a dense contraction on the matrix cores:
+//
+//   * block tile 128 (M) x 16*NT (N), 4 waves, 1 block per CU.  For the
+//     Qwen intermediate size N = 17408 = 64 * 272 the planner picks NT = 17,
+//     so M = 512 gives exactly 4 * 64 = 256 blocks: one per CU, no tail.
+//   * wave w owns N-tiles w*NQ .. w*NQ+NQ-1 for all 8 M-tiles, plus M-tiles
+//     2w, 2w+1 of each of the NR leftover N-tiles (NT = 4*NQ + NR): every
+//     wave issues the same 8*NQ + 2*NR MFMAs per k-step.
+//   * per 128-k group, X (128 x 128 fp16) and the block's packed weights
+//     (16*NT rows x 64 bytes) are copied global -> LDS by the DMA path
+//     (global_load_lds_dwordx4), three groups deep, so no VGPRs hold
+//     in-flight data.  One barrier per group.
+//   * each wave decodes only its own weight rows from LDS: two's-complement
+//     nibbles -> exact fp16 integers (byte permute + one v_bitop3_b32 + one
+//     v_pk_fma_f16 per pair), times the fp16 group scale (v_pk_mul_f16),
+//     straight into the B operand of v_mfma_f32_16x16x32_f16 (FP32
+//     accumulation).  The product q*s is rounded to fp16 once per weight
+//     (relative error <= 2^-11), the usual W4A16 trade: it keeps the 136
+//     accumulators per lane in VGPRs.  Dequantisation itself (fp32 q*s) stays
+//     bit-exact in xinfer_dequant_int4_f32.
+//   * epilogue: bias / fp16 or fp32 store, or SiLU(gate) * up when the block
+//     holds paired gate and up tiles (SwiGLU prefill).
+
+#include <mutex>
 
 #include "common.h"
 
+namespace xhip {
+
+struct GemmParams {
+    const f16* X;          // [M][K]
+    const uint8_t* W;      // [N][K/2]   (gate for SwiGLU)
+    const uint16_t* S;     // [N][K/128]
+    const uint8_t* W2;     // up (SwiGLU)
+    const uint16_t* S2;
+    const float* bias;     // optional [N]
+    void* Y;               // [M][N]
+    int32_t M, N, K;
+    int32_t mblocks, nranges;
+    int32_t xcd_map;       // 1: XCD-aware block -> tile mapping
+};
+
+constexpr int kGM = 128;      // block rows
+constexpr int kStages = 3;    // groups in flight through LDS
+
+// Natural-order decode of one dword (8 nibbles, k0 in bits 0-3) into four
+// fp16 pairs (k0,k1) (k2,k3) (k4,k5) (k6,k7) of exact integers.  A byte
+// permute puts byte b (nibbles k_2b, k_2b+1) in the low byte of both halves;
+// "mask, flip bit 3, OR 0x6400" is one v_bitop3_b32 giving (1024 + u_lo,
+// 1024 + 16 u_hi) with u = q + 8; one packed fma removes the per-half bias.
+__device__ __forceinline__ void decode8_natural(uint32_t w, f16x2 q[4]) {
+    const f16x2 kMul = {(f16)1.0f, (f16)0.0625f};
+    const f16x2 kAdd = {(f16)-1032.0f, (f16)-72.0f};
+    const uint32_t b0 = __builtin_amdgcn_perm(w, w, 0x0C000C00u);  // [b0, 0, b0, 0]
+    const uint32_t b1 = __builtin_amdgcn_perm(w, w, 0x0C010C01u);  // [b1, 0, b1, 0]
+    const uint32_t b2 = __builtin_amdgcn_perm(w, w, 0x0C020C02u);
+    const uint32_t b3 = __builtin_amdgcn_perm(w, w, 0x0C030C03u);
+    q[0] = as_h2((b0 & 0x00F0000Fu) ^ 0x64806408u) * kMul + kAdd;
+    q[1] = as_h2((b1 & 0x00F0000Fu) ^ 0x64806408u) * kMul + kAdd;
+    q[2] = as_h2((b2 & 0x00F0000Fu) ^ 0x64806408u) * kMul + kAdd;
+    q[3] = as_h2((b3 & 0x00F0000Fu) ^ 0x64806408u) * kMul + kAdd;
+}
+
+__device__ __forceinline__ f16x8 pack8(const f16x2 q[4]) {
+    f16x8 r;
+    r[0] = q[0].x; r[1] = q[0].y; r[2] = q[1].x; r[3] = q[1].y;
+    r[4] = q[2].x; r[5] = q[2].y; r[6] = q[3].x; r[7] = q[3].y;
+    return r;
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+__device__ __forceinline__ void dma16(const void* g, unsigned char* lds_wave_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr_t)lds_wave_base, 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(n) leaving the other counters alone (gfx9 encoding).
+#define XHIP_WAIT_VMCNT(n) \
+    __builtin_amdgcn_s_waitcnt(((n) & 0xF) | (((n) >> 4) << 14) | (0x7 << 4) | (0xF << 8))
+
+constexpr int kWavesG = 8;   // waves per GEMM block (2 per SIMD)
+
+template <int NQ, int NR, int EPI, typename OutT>
+__global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p) {
+    constexpr bool SWIGLU = (EPI == 1);
+    static_assert(!SWIGLU || NR == 0, "SwiGLU tiles pair gate/up per wave");
+    constexpr int NW = kWavesG;
+    constexpr int NT = SWIGLU ? 2 * NW * NQ : NW * NQ + NR;  // weight tiles (16 rows) per block
+    constexpr int OWN = SWIGLU ? 2 * NQ : NQ;                // full-M tiles per wave
+    constexpr int WPW = (NT + NW - 1) / NW;                  // weight DMA loads per wave per group
+    constexpr int X_BYTES = kGM * 128 * 2;                   // 32 KB
+    constexpr int W_BYTES = (NT + 1) * 1024;                 // + one shared spare slot
+    constexpr int STAGE = X_BYTES + W_BYTES;
+    constexpr int NSC = OWN + NR;                            // B operands per wave per step
+    constexpr int SROWS = 16 * NT;                           // weight rows of the block
+    constexpr int SWL = (SROWS + 64 * NW - 1) / (64 * NW);  // scale DMA loads per wave per chunk
+    constexpr int SC_BYTES = SROWS * 16;                     // one 8-group scale chunk
+    constexpr int XPW = 32 / NW;                             // X DMA loads per wave per group
+
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int li = lane & 15, lj = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    // block -> (M block, N range); XCD-aware when the grid allows it, so the
+    // blocks on one XCD share one M block of X in that XCD's L2
+    int mb, nr;
+    const int b = blockIdx.x;
+    if (p.xcd_map) {
+        const int per = 8 / p.mblocks;
+        const int xcd = b & 7, s = b >> 3;
+        mb = xcd % p.mblocks;
+        nr = s * per + xcd / p.mblocks;
+    } else {
+        mb = b % p.mblocks;
+        nr = b / p.mblocks;
+    }
+    const int M = p.M, N = p.N, K = p.K;
+    const int m0 = mb * kGM;
+    const int ncol = SWIGLU ? 16 * NW * NQ : 16 * NT;  // output columns per block
+    const int n0 = nr * ncol;
+    const int ng = K >> 7;
+    const size_t row_bytes = (size_t)(K >> 1);
+
+    // --- DMA sources (per lane, group 0) -------------------------------------
+    // X: wave-load wl (0..31) covers chunk q = wl*64 + lane of the layout
+    // [t][mt][lj][li] (16 bytes = 8 consecutive k of one row).
+    const f16* xsrc[XPW];
+#pragma unroll
+    for (int i = 0; i < XPW; ++i) {
+        const int wl = wave * XPW + i;
+        const int mt = wl & 7, t = wl >> 3;
+        const int row = min(m0 + mt * 16 + li, M - 1);
+        xsrc[i] = p.X + (size_t)row * K + 32 * lj + 8 * t;
+    }
+    // W: tile tt = wave + NW*i; lane copies 16 bytes (k 32*lj .. +32 of the
+    // group) of row (tile base + li).  Waves with no tile left re-copy tile 0
+    // into the spare slot so every wave issues the same number of loads.
+    auto tile_row = [&](int tt, const uint8_t** base) -> int {
+        if (SWIGLU) {
+            const int half = tt >= NW * NQ;
+            *base = half ? p.W2 : p.W;
+            return n0 + (tt - half * NW * NQ) * 16;
+        }
+        *base = p.W;
+        return n0 + tt * 16;
+    };
+    const uint8_t* wsrc[WPW];
+#pragma unroll
+    for (int i = 0; i < WPW; ++i) {
+        const int tt = wave + NW * i;
+        const uint8_t* base;
+        const int row = min(tile_row(tt < NT ? tt : 0, &base) + li, N - 1);
+        wsrc[i] = base + (size_t)row * row_bytes + 16 * lj;
+    }
+    // Scales travel in chunks of 8 groups: row r's 16 bytes S[r][8c .. 8c+7]
+    // land in scale buffer c%2 at slot r (the host requires K % 1024 == 0,
+    // which makes every such piece 16-byte aligned).
+    const uint16_t* ssrc[SWL];
+#pragma unroll
+    for (int i = 0; i < SWL; ++i) {
+        const int r = 64 * (wave + NW * i) + lane;
+        const int rr = r < SROWS ? r : 0;
+        const uint8_t* wb;
+        const int row = min(tile_row(rr >> 4, &wb) + (rr & 15), N - 1);
+        const uint16_t* base = (SWIGLU && wb == p.W2) ? p.S2 : p.S;
+        ssrc[i] = base + (size_t)row * ng;
+    }
+    // LDS slots of the tiles this wave decodes: own full tiles, then leftovers
+    int wslot[NSC];
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) {
+        if (SWIGLU) wslot[i] = (i < NQ) ? wave * NQ + i : NW * NQ + wave * NQ + (i - NQ);
+        else wslot[i] = i < NQ ? wave * NQ + i : NW * NQ + (i - NQ);
+    }
+    int sslot[NSC];
+#pragma unroll
+    for (int i = 0; i < NSC; ++i) sslot[i] = (wslot[i] * 16 + li) * 16;
+
+    auto issue_dma = [&](int g, int stage) {
+        unsigned char* st = smem + stage * STAGE;
+        const int gg = g < ng ? g : ng - 1;  // past the end: harmless re-load
+#pragma unroll
+        for (int i = 0; i < XPW; ++i)
+            dma16(xsrc[i] + (size_t)gg * 128, st + (wave * XPW + i) * 1024);
+#pragma unroll
+        for (int i = 0; i < WPW; ++i) {
+            const int tt = wave + NW * i;
+            dma16(wsrc[i] + (size_t)gg * 64, st + X_BYTES + (tt < NT ? tt : NT) * 1024);
+        }
+    };
+    unsigned char* const sbuf = smem + kStages * STAGE;  // 2 x SC_BYTES
+    auto issue_scale_chunk = [&](int c) {
+        const int cc = c * 8 < ng ? c : (ng >> 3) - 1;
+#pragma unroll
+        for (int i = 0; i < SWL; ++i) {
+            const int r0 = 64 * (wave + NW * i);
+            if (r0 < SROWS && r0 + lane < SROWS)  // lanes past the block's rows stay idle
+                dma16(ssrc[i] + cc * 8, sbuf + (c & 1) * SC_BYTES + r0 * 16);
+        }
+    };
+    constexpr int DPG = XPW + WPW;  // DMA loads per wave per group
+
+    f32x4 acc[8][OWN > 0 ? OWN : 1];
+    f32x4 accL[NR > 0 ? NR : 1];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int i = 0; i < (OWN > 0 ? OWN : 1); ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < (NR > 0 ? NR : 1); ++r) accL[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    issue_scale_chunk(0);
+    issue_dma(0, 0);
+    issue_dma(1, 1);
+
+    auto make_b = [&](const u32x4& w, int t, f16x2 s2) -> f16x8 {
+        f16x2 q[4];
+        decode8_natural(w[t], q);
+        q[0] *= s2;
+        q[1] *= s2;
+        q[2] *= s2;
+        q[3] *= s2;
+        return pack8(q);
+    };
+
+    // One group = 4 k-steps; per step the wave issues 8*OWN + NR MFMAs.
+    // Leftover tile r: this wave does M-tile `wave` only.
+    auto compute_group = [&](int stage, int g) {
+        const unsigned char* st = smem + stage * STAGE;
+        const unsigned char* sc = sbuf + ((g >> 3) & 1) * SC_BYTES + (g & 7) * 2;
+        u32x4 wv[NSC];
+        f16x2 s2[NSC];
+#pragma unroll
+        for (int i = 0; i < NSC; ++i) {
+            wv[i] = *reinterpret_cast<const u32x4*>(st + X_BYTES + wslot[i] * 1024 + lane * 16);
+            const f16 s = *reinterpret_cast<const f16*>(sc + sslot[i]);
+            s2[i] = f16x2{s, s};
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const unsigned char* xt = st + (t * 8) * 1024 + lane * 16;
+            f16x8 a[8];
+            if (OWN > 0) {
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt) a[mt] = *reinterpret_cast<const f16x8*>(xt + mt * 1024);
+            }
+            f16x8 aw = *reinterpret_cast<const f16x8*>(xt + wave * 1024);
+#pragma unroll
+            for (int i = 0; i < NSC; ++i) {
+                const f16x8 bop = make_b(wv[i], t, s2[i]);
+                if (i < OWN) {
+#pragma unroll
+                    for (int mt = 0; mt < 8; ++mt)
+                        acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], bop, acc[mt][i], 0, 0, 0);
+                } else {
+                    accL[i - OWN] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw, bop, accL[i - OWN], 0, 0, 0);
+                }
+            }
+        }
+    };
+
+    // vmcnt(DPG) waits for everything but the newest DPG loads (DMA(g+1)):
+    // DMA(g) and any scale chunk issued before it have landed.
+    auto step_group = [&](int g, const int j) {
+        XHIP_WAIT_VMCNT(DPG);
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): reads of stage g-1 done
+        __builtin_amdgcn_s_barrier();
+        // chunk c+1 of the scales is fetched at group 8c+1 into the buffer
+        // chunk c-1 used (all waves are past group 8c by this barrier)
+        if ((g & 7) == 1) issue_scale_chunk((g >> 3) + 1);
+        issue_dma(g + 2, (j + 2) % kStages);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_group(j, g);
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    // Main loop over whole triplets (stage indices are constants and there
+    // is no branch around a load with a VGPR result, so the compiler's own
+    // vmcnt bookkeeping stays exact); then the 0-2 remaining groups.
+    int g = 0;
+    for (; g + kStages <= ng; g += kStages) {
+        step_group(g, 0);
+        step_group(g + 1, 1);
+        step_group(g + 2, 2);
+    }
+    if (g < ng) step_group(g, 0);
+    if (g + 1 < ng) step_group(g + 1, 1);
+    XHIP_WAIT_VMCNT(0);
+
+    // --- epilogue ------------------------------------------------------------
+    // D layout of v_mfma_f32_16x16x32_f16: lane l holds rows 4*(l/16)+e,
+    // e = 0..3, of column l%16.
+    auto store = [&](int m, int n, float v) {
+        if (m < M && n < N) reinterpret_cast<OutT*>(p.Y)[(size_t)m * N + n] = (OutT)v;
+    };
+    auto bias_of = [&](int n) -> float { return (!SWIGLU && p.bias && n < N) ? p.bias[n] : 0.0f; };
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        const int n = n0 + (wave * NQ + i) * 16 + li;
+        const float bn = bias_of(n);
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = m0 + mt * 16 + 4 * lj + e;
+                float v = acc[mt][i][e] + bn;
+                if (SWIGLU) {
+                    const float u = acc[mt][NQ + i][e];
+                    v = v / (1.0f + expf(-v)) * u;
+                }
+                store(m, n, v);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        const int n = n0 + (NW * NQ + r) * 16 + li;
+        const float bn = bias_of(n);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store(m0 + wave * 16 + 4 * lj + e, n, accL[r][e] + bn);
+    }
+}
+
+}  // namespace xhip
+
+// ------------------------------------------------------------------ host ----
+
+using namespace xhip;
+
+namespace {
+
+typedef void (*GemmKernel)(GemmParams);
+
+struct GemmCfg {
+    int nq, nr;
+};
+
+template <int EPI, typename OutT>
+GemmKernel gemm_kernel_for(int nq, int nr) {
+    if (EPI == 1) return gemm_int4_mfma_kernel<1, 0, 1, OutT>;
+    if (nq == 2 && nr == 1) return gemm_int4_mfma_kernel<2, 1, 0, OutT>;
+    if (nq == 2) return gemm_int4_mfma_kernel<2, 0, 0, OutT>;
+    if (nq == 1) return gemm_int4_mfma_kernel<1, 0, 0, OutT>;
+    return gemm_int4_mfma_kernel<0, 4, 0, OutT>;
+}
+
+size_t gemm_lds_bytes(int nt) {
+    return (size_t)kStages * (kGM * 128 * 2 + (nt + 1) * 1024) + 2 * (size_t)(16 * nt * 16);
+}
+
+template <int EPI, typename OutT>
+int launch_gemm(hipStream_t st, GemmParams& p) {
+    // Candidate N tiles (16-column MFMA tiles per block).  Estimated time =
+    // rounds of one-block-per-CU waves x work per block.
+    const int cus = xhip_host::num_cus();
+    const GemmCfg cands_plain[] = {{2, 1}, {2, 0}, {1, 0}, {0, 4}};
+    const GemmCfg cands_swiglu[] = {{1, 0}};
+    const GemmCfg* cands = EPI == 1 ? cands_swiglu : cands_plain;
+    const int ncand = EPI == 1 ? 1 : 4;
+    const int mblocks = (p.M + kGM - 1) / kGM;
+    GemmCfg best = cands[0];
+    double best_cost = 1e300;
+    for (int i = 0; i < ncand; ++i) {
+        const int nt = EPI == 1 ? kWavesG * cands[i].nq : kWavesG * cands[i].nq + cands[i].nr;
+        const int64_t nranges = (p.N + 16 * nt - 1) / (16 * nt);
+        const int64_t blocks = mblocks * nranges;
+        const int64_t rounds = (blocks + cus - 1) / cus;
+        const double cost = (double)rounds * nt * (1.0 + 0.5 / nt);  // + per-block overhead
+        if (cost < best_cost) { best_cost = cost; best = cands[i]; }
+    }
+    const int nt_w = EPI == 1 ? 2 * kWavesG * best.nq : kWavesG * best.nq + best.nr;  // weight tiles
+    const int ncol = EPI == 1 ? 16 * kWavesG * best.nq : 16 * nt_w;
+    p.mblocks = mblocks;
+    p.nranges = (p.N + ncol - 1) / ncol;
+    const int blocks = p.mblocks * p.nranges;
+    p.xcd_map = (8 % p.mblocks == 0) && (blocks % 8 == 0) ? 1 : 0;
+    GemmKernel k = gemm_kernel_for<EPI, OutT>(best.nq, best.nr);
+    const size_t lds = gemm_lds_bytes(nt_w);
+    static std::mutex mu;
+    static GemmKernel configured[16];
+    static int nconf = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        bool done = false;
+        for (int i = 0; i < nconf; ++i) done |= configured[i] == k;
+        if (!done) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(k),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+                return XINFER_ERR_HIP;
+            if (nconf < 16) configured[nconf++] = k;
+        }
+    }
+    hipLaunchKernelGGL(k, dim3(blocks), dim3(64 * kWavesG), lds, st, p);
+    return xhip_host::launch_status();
+}
+
+}  // namespace
+
 namespace xhip_host {
 
-int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
-                  const uint16_t* S, const uint8_t* W2, const uint16_t* S2, const float* bias,
-                  int64_t M, int64_t N, int64_t K) {
+// M > 8 with K % 1024 != 0: the MFMA kernel's 8-group scale chunks would not
+// be 16-byte aligned, so these shapes run the GEMV kernels on slabs of 8
+// activation rows instead (correct, not tuned).
+int gemm_by_gemv_slabs(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
+                       const uint16_t* S, const uint8_t* W2, const uint16_t* S2,
+                       const float* bias, int64_t M, int64_t N, int64_t K) {
     const size_t ysz = y_f32 ? 4 : 2;
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mm = (M - m0) < 8 ? (M - m0) : 8;
@@ -24,6 +427,25 @@ int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint
         if (rc) return rc;
     }
     return XINFER_OK;
+}
+
+int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
+                  const uint16_t* S, const uint8_t* W2, const uint16_t* S2, const float* bias,
+                  int64_t M, int64_t N, int64_t K) {
+    if (K % 1024 != 0) return gemm_by_gemv_slabs(st, Y, y_f32, X, W, S, W2, S2, bias, M, N, K);
+    GemmParams p = {};
+    p.X = reinterpret_cast<const f16*>(X);
+    p.W = W;
+    p.S = S;
+    p.W2 = W2;
+    p.S2 = S2;
+    p.bias = bias;
+    p.Y = Y;
+    p.M = (int32_t)M;
+    p.N = (int32_t)N;
+    p.K = (int32_t)K;
+    if (W2) return launch_gemm<1, f16>(st, p);
+    return y_f32 ? launch_gemm<0, float>(st, p) : launch_gemm<0, f16>(st, p);
 }
 
 }  // namespace xhip_host

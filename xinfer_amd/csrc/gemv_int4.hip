@@ -34,6 +34,8 @@
 
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "common.h"
 
 namespace xhip {
@@ -513,69 +515,97 @@ int blocks_per_cu(GemvKernel k, size_t lds) {
     return v;
 }
 
-// Choose rows per item (R), rows per block and the grid.  Each block runs
-// ceil(rows_blk / R) * nsteps items over 8 teams; the estimated time is the
-// number of grid rounds times the busiest team's bytes (+ a per-item cost).
+// Choose rows per item (R), rows per block and the grid.  Measured on
+// MI355X (north-star, config-0/1/2/3 shapes, graph-replayed): two resident
+// 256-thread blocks per CU, R = 2 and a one-item prefetch ring are best for
+// M = 1; larger M keeps a two-item ring.  Each block runs
+// (rows_blk / 2R) * nsteps items over its 4 waves.  Plans are cached per
+// (epilogue, M, K, N of each descriptor) so repeated calls skip this.
+struct PlanKey {
+    int epi, mr, K, ndesc;
+    int32_t N[4];
+    bool operator==(const PlanKey& o) const {
+        return epi == o.epi && mr == o.mr && K == o.K && ndesc == o.ndesc && N[0] == o.N[0] &&
+               N[1] == o.N[1] && N[2] == o.N[2] && N[3] == o.N[3];
+    }
+};
+struct PlanEntry {
+    PlanKey key;
+    GemvPlan plan;
+    int32_t rows_blk;
+    int dev;
+};
+
 template <int EPI, typename OutT>
 GemvPlan plan_gemv(GemvParams& p, int mr) {
-    const int K = p.K;
-    const int cpr = K / 32;
-    const int nsteps = (cpr + 31) / 32;
-    const int E = EPI == EPI_SWIGLU ? 2 : 1;
-    const int cus = xhip_host::num_cus();
-    int64_t total_rows = 0;
-    for (int i = 0; i < p.ndesc; ++i) total_rows += p.d[i].N;
-    const size_t x_bytes = (size_t)mr * nsteps * 32 * (64 + 4);
-    const bool xlds = x_bytes + 4096 <= 64 * 1024;
-
-    const int rcands[3] = {1, 2, 4};
-    const Overrides& ov = overrides();
-    const int pf = ov.pf > 0 ? ov.pf : 2;
+    PlanKey key = {EPI, mr, p.K, p.ndesc, {0, 0, 0, 0}};
+    for (int i = 0; i < p.ndesc; ++i) key.N[i] = p.d[i].N;
+    int dev = 0;
+    (void)hipGetDevice(&dev);
+    static PlanEntry cache[64];
+    static int ncache = 0;
+    static std::mutex mu;
     GemvPlan best = {};
-    double best_cost = 1e300;
-    for (int ri = 0; ri < 3; ++ri) {
-        const int r = rcands[ri];
-        if ((mr == 2 && r == 1) || (mr >= 4 && r == 4)) continue;
-        if (ov.r > 0 && ov.r != r) continue;
+    int32_t rows_blk = 0;
+    bool hit = false;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        for (int i = 0; i < ncache; ++i)
+            if (cache[i].dev == dev && cache[i].key == key) {
+                best = cache[i].plan;
+                rows_blk = cache[i].rows_blk;
+                hit = true;
+                break;
+            }
+    }
+    if (!hit) {
+        const int K = p.K;
+        const int cpr = K / 32;
+        const int nsteps = (cpr + 31) / 32;
+        const int E = EPI == EPI_SWIGLU ? 2 : 1;
+        const int cus = xhip_host::num_cus();
+        int64_t total_rows = 0;
+        for (int i = 0; i < p.ndesc; ++i) total_rows += p.d[i].N;
+        const size_t x_bytes = (size_t)mr * nsteps * 32 * (64 + 4);
+        const bool xlds = x_bytes + 4096 <= 64 * 1024;
+        const Overrides& ov = overrides();
+        const int r = ov.r > 0 ? ov.r : (mr >= 4 && !xlds ? 1 : 2);
+        const int pf = ov.pf > 0 ? ov.pf : (mr == 1 ? 1 : 2);
         GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf);
-        // first guess of residency with a small partial area, then refine once
-        size_t lds = (xlds ? x_bytes : 0) + 4096;
-        int bpc = ov.bpc > 0 ? ov.bpc : blocks_per_cu(k, lds);
-        for (int pass = 0; pass < 2; ++pass) {
+        int64_t rows = 0;
+        size_t lds = 0;
+        int bpc = ov.bpc > 0 ? ov.bpc : 2;
+        for (int pass = 0; pass < 3; ++pass) {
             const int64_t target = (int64_t)cus * bpc;
-            int64_t rows_blk = (total_rows + target - 1) / target;
-            rows_blk = ((rows_blk + 2 * r - 1) / (2 * r)) * (2 * r);
-            if (rows_blk < 2 * r) rows_blk = 2 * r;
-            size_t part = (size_t)rows_blk * mr * E * nsteps * 4;
+            rows = (total_rows + target - 1) / target;
+            rows = ((rows + 2 * r - 1) / (2 * r)) * (2 * r);
+            size_t part = (size_t)rows * mr * E * nsteps * 4;
             if (EPI == EPI_ARGMAX && part < 2048) part = 2048;
             lds = (xlds ? x_bytes : 0) + part;
-            if (lds > 64 * 1024) { lds = 0; break; }  // not placeable: skip this R
-            const int bpc2 = ov.bpc > 0 ? ov.bpc : blocks_per_cu(k, lds);
-            if (pass == 0 && bpc2 != bpc) { bpc = bpc2; continue; }
-            int64_t blocks = 0;
-            for (int i = 0; i < p.ndesc; ++i) blocks += (p.d[i].N + rows_blk - 1) / rows_blk;
-            const int64_t rounds = (blocks + (int64_t)cus * bpc2 - 1) / ((int64_t)cus * bpc2);
-            const int64_t items = (rows_blk / (2 * r)) * nsteps;
-            const int64_t per_wave = (items + 3) / 4;
-            const double cost = (double)rounds * per_wave * (2 * r + 1.5);
-            if (cost < best_cost * 0.98 || (cost <= best_cost * 1.02 && r > best.r)) {
-                best_cost = cost;
-                best.mr = mr;
-                best.r = r;
-                best.xlds = xlds;
-                best.lds = lds;
-                best.pf = pf;
-                best.blocks = (int)blocks;
-                for (int i = 0; i < p.ndesc; ++i) p.d[i].rows_blk = (int32_t)rows_blk;
-            }
-            break;
+            if (lds <= 64 * 1024) break;
+            bpc *= 2;  // smaller row ranges until the partial slots fit
         }
+        const int occ = blocks_per_cu(k, lds);
+        if (ov.bpc <= 0 && occ < bpc) {  // cannot hold the target residency
+            const int64_t target = (int64_t)cus * occ;
+            int64_t r2 = (total_rows + target - 1) / target;
+            r2 = ((r2 + 2 * r - 1) / (2 * r)) * (2 * r);
+            if ((size_t)r2 * mr * E * nsteps * 4 + (xlds ? x_bytes : 0) <= 64 * 1024) rows = r2;
+        }
+        best.mr = mr;
+        best.r = r;
+        best.pf = pf;
+        best.xlds = xlds;
+        best.lds = lds;
+        rows_blk = (int32_t)rows;
+        std::lock_guard<std::mutex> lock(mu);
+        if (ncache < 64) cache[ncache++] = PlanEntry{key, best, rows_blk, dev};
     }
-    // assign block ranges with the winning rows_blk
     int blocks = 0;
     for (int i = 0; i < p.ndesc; ++i) {
+        p.d[i].rows_blk = rows_blk;
         p.d[i].block_begin = blocks;
-        blocks += (p.d[i].N + p.d[i].rows_blk - 1) / p.d[i].rows_blk;
+        blocks += (p.d[i].N + rows_blk - 1) / rows_blk;
     }
     for (int i = p.ndesc; i < 4; ++i) p.d[i] = p.d[0], p.d[i].block_begin = 0x7FFFFFFF;
     best.blocks = blocks;
