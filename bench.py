@@ -3,15 +3,21 @@
 Headline (one JSON line on stdout): BASELINE config 1 -- the decode MLP
 gate/up projection with the SiLU epilogue, M=1, K=5120, 2 x 17408 rows in
 one interleaved packed-INT4 matrix (W_up = W_gate + 17408*2560 bytes),
-17408 fp16 outputs.  One "step" = one launch over one batch.  The value is
+17408 fp16 outputs.  One "step" = one launch over one batch.  `value` is
 HBM GB/s of algorithmic bytes N*K/2 + N*(K/128)*2 + M*K*2 + M*N_out*2 per
-step divided by the wall time per step, with all inputs resident in HBM
-and the weights rotated over enough copies (> 512 MB) that the 256 MB
-Infinity Cache cannot hold them.
+step divided by the wall time per step, all inputs resident in HBM and the
+weights rotated over enough copies (> 600 MB) that the 256 MB Infinity
+Cache cannot hold them.  Launches are replayed from a HIP graph (how a
+decode step is issued; the reference does the same with a SYCL graph,
+src/targets/qwen3_8/decode_graph.cpp), so host launch cost is not timed.
 
-The other BASELINE configs are measured the same way and reported under
-"suite" (disable with --quick).  The CPU baseline is the oracle restatement
-of the reference CPU loop, timed on this host.
+The other BASELINE configs are measured the same way under "suite"
+(--quick skips them).  The CPU baseline is the oracle restatement of the
+reference CPU loop, timed on this host's cores.
+
+    python bench.py                       # default: N=1, all configs
+    python bench.py --only cfg1 --no-cpu  # one config (profiling runs)
+    python bench.py --calib-copy          # plain copy of known size (PMC scale)
 """
 from __future__ import annotations
 
@@ -21,8 +27,6 @@ import os
 import sys
 import time
 
-import numpy as np
-
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
@@ -30,9 +34,11 @@ HBM_PEAK_GBPS = 8000.0          # MI355X published HBM3E bandwidth
 FP16_PEAK_TFLOPS = 2500.0       # MI355X published dense FP16 MFMA
 MALL_BYTES = 256 << 20
 ROTATE_MIN_BYTES = 600 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_config1_gate_up_m1.json")
 
 
 def gemv_bytes(M, Nrows, K, Nout, out_bytes):
+    """Algorithmic bytes of one INT4-G128 projection launch."""
     return Nrows * K // 2 + Nrows * (K // 128) * 2 + M * K * 2 + M * Nout * out_bytes
 
 
@@ -49,7 +55,6 @@ class Rig:
 
     def __init__(self, torch, dev, Nrows, K, sigma, seed=0):
         from xinfer_amd import synth
-        self.torch = torch
         W = synth.packed_weights(seed, Nrows, K)
         S = synth.scales(seed, Nrows, K, sigma)
         one = Nrows * K // 2 + Nrows * (K // 128) * 2
@@ -58,16 +63,9 @@ class Rig:
         s0 = torch.from_numpy(S).view(torch.float16).to(dev)
         self.W = [w0] + [w0.clone() for _ in range(self.copies - 1)]
         self.S = [s0] + [s0.clone() for _ in range(self.copies - 1)]
-        self.host_W, self.host_S = W, S
 
 
-def time_launches(torch, launch, steps, warmup, copies, graph=False):
-    """Time `steps` launches rotating over `copies` weight copies.  Returns
-    (wall seconds per step, event seconds per step).  graph=True captures one
-    rotation of launches into a HIP graph (the way a decode step is replayed)
-    and times replays, which removes host launch overhead."""
-    if graph:
-        return _time_graph(torch, launch, steps, warmup, copies)
+def _time_eager(torch, launch, steps, warmup, copies):
     for i in range(warmup):
         launch(i % copies)
     torch.cuda.synchronize()
@@ -108,21 +106,35 @@ def _time_graph(torch, launch, steps, warmup, copies):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     n = reps * per
-    return wall / n, e0.elapsed_time(e1) * 1e-3 / n
+    return wall / n, e0.elapsed_time(e1) * 1e-3 / n, n
+
+
+def time_launches(torch, launch, steps, warmup, copies, graph=False):
+    """(wall s/step, event s/step) for `steps` launches rotating weight copies.
+    graph=True captures one rotation into a HIP graph and times replays.
+    The events are recorded on the stream the kernels run on."""
+    if graph:
+        w, e, _ = _time_graph(torch, launch, steps, warmup, copies)
+        return w, e
+    return _time_eager(torch, launch, steps, warmup, copies)
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--steps", type=int, default=640)
+    ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--quick", action="store_true", help="headline config only")
+    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="run a plain 256 MiB device copy 20x (PMC calibration) and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print("bench.py measures one GPU only: this build's projection path is a "
+        print("bench.py measures one GPU only: this build's INT4 projection path is a "
               "single-GPU kernel (multi-GPU sharding is design-only); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
@@ -134,35 +146,58 @@ def main():
     dev = torch.device("cuda:0")
     log = lambda *a: print(*a, file=sys.stderr, flush=True)  # noqa: E731
 
+    if args.calib_copy:
+        n = 256 << 20
+        a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(20):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log(f"copied {n} bytes x 20")
+        return
+
+    only = set(x for x in args.only.split(",") if x)
+    want = lambda k: (not only) or (k in only)  # noqa: E731
+    graph = not args.eager
+
     # ---------------- headline: config 1, fused gate/up + SiLU, M=1 ----------------
     M, N, K = 1, 17408, 5120
-    rig = Rig(torch, dev, 2 * N, K, 0.02)
-    Xb = synth.activations(0, M, K)
-    X = torch.from_numpy(Xb).view(torch.float16).to(dev)
-    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
-
-    def launch_cfg1(i):
-        W, S = rig.W[i], rig.S[i]
-        ops.mlp_gate_up_swiglu_int4(Y, X, W[:N], S[:N], W[N:], S[N:], M, N, K)
-
-    copies = rig.copies
-    log(f"config 1: M={M} K={K} N=2x{N}, {copies} weight copies")
-    wall_step, ev_step = time_launches(torch, launch_cfg1, args.steps, args.warmup, rig.copies)
     nbytes = gemv_bytes(M, 2 * N, K, N, 2)
-    value = nbytes / wall_step / 1e9
-    achieved = nbytes / ev_step / 1e9
-    log(f"  wall {wall_step*1e6:.2f} us/step, events {ev_step*1e6:.2f} us/launch, "
-        f"{achieved:.0f} GB/s")
-    del rig
+    head = None
+    if want("cfg1"):
+        rig = Rig(torch, dev, 2 * N, K, 0.02)
+        X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+        Y = torch.empty((M, N), dtype=torch.float16, device=dev)
 
-    suite = {}
-    if not args.quick:
-        suite = run_suite(torch, dev, ops, synth, args, log)
+        def launch_cfg1(i):
+            W, S = rig.W[i], rig.S[i]
+            ops.mlp_gate_up_swiglu_int4(Y, X, W[:N], S[:N], W[N:], S[N:], M, N, K)
+
+        wall_step, ev_step = time_launches(torch, launch_cfg1, args.steps, args.warmup,
+                                           rig.copies, graph=graph)
+        head = (wall_step, ev_step, rig.copies)
+        log(f"config 1: M={M} K={K} N=2x{N}, {rig.copies} weight copies, "
+            f"wall {wall_step*1e6:.2f} us/step, events {ev_step*1e6:.2f} us/launch, "
+            f"{nbytes/ev_step/1e9:.0f} GB/s")
+        del rig
+
+    suite = {} if args.quick else run_suite(torch, dev, ops, synth, args, log, want, graph)
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and head is not None:
         cpu = cpu_baseline(nbytes, log)
 
+    if head is None:
+        print(json.dumps({"suite": suite}), flush=True)
+        return
+    wall_step, ev_step, copies = head
+    value = nbytes / wall_step / 1e9
+    achieved = nbytes / ev_step / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        traffic = t.get("hbm_bytes_per_launch")
     line = {
         "metric": "INT4 GEMV HBM GB/s (% of MI355X peak) at M=1; prefill GEMM TFLOP/s at M=512",
         "value": round(value, 1),
@@ -174,15 +209,16 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int4xf16->f32acc",
+        "dtype": "int4 x f16 -> f32 accumulate",
         "data": "synthetic (SplitMix64 seed 0: uniform int4, |N(0,0.02)|/7 fp16 scales, N(0,1) fp16 x)",
-        "config": {"workload": "config1 fused gate/up SiLU decode GEMV", "M": M, "K": K,
-                   "N": f"2x{N}", "group_size": 128, "weight_copies_rotated": copies,
-                   "parallelism": "single GPU"},
+        "config": {"workload": "BASELINE config 1: fused gate/up SiLU decode GEMV",
+                   "M": M, "K": K, "N": f"2x{N}", "group_size": 128,
+                   "weight_copies_rotated": copies,
+                   "launch": "hip graph replay" if graph else "eager"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None,
-                     "kernel": "gemv_int4_kernel<MR=1,R=4,EPI_SWIGLU>",
+                     "traffic": traffic,
+                     "kernel": "xhip::gemv_int4_kernel<MR=1,R=2,EPI_SWIGLU,...,PF=1>",
                      "algorithmic_bytes_per_launch": nbytes,
                      "avg_launch_us": round(ev_step * 1e6, 3)},
         "cpu_baseline": cpu,
@@ -191,64 +227,71 @@ def main():
     print(json.dumps(line), flush=True)
 
 
-def run_suite(torch, dev, ops, synth, args, log):
+def run_suite(torch, dev, ops, synth, args, log, want, graph):
     out = {}
-    steps = max(20, min(args.steps, 200))
-    warm = min(args.warmup, 20)
+    steps = max(64, min(args.steps, 512))
+    warm = min(args.warmup, 32)
+
+    def record(name, d):
+        out[name] = d
+        log(f"  {name}: {d}")
 
     def gemv_cfg(name, M, N, K, sigma=0.02):
         rig = Rig(torch, dev, N, K, sigma)
         X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
         Y = torch.empty((M, N), dtype=torch.float16, device=dev)
         fn = lambda i: ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)  # noqa: E731
-        w, e = time_launches(torch, fn, steps, warm, rig.copies)
+        w, e = time_launches(torch, fn, steps, warm, rig.copies, graph=graph)
         b = gemv_bytes(M, N, K, N, 2)
-        out[name] = {"M": M, "N": N, "K": K, "us": round(e * 1e6, 3), "GBps": round(b / e / 1e9, 1),
-                     "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)}
-        log(f"  {name}: {out[name]}")
+        record(name, {"M": M, "N": N, "K": K, "us": round(e * 1e6, 3),
+                      "GBps": round(b / e / 1e9, 1), "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)})
 
-    gemv_cfg("northstar_gemv_m1_n34816_k5120", 1, 34816, 5120)
-    gemv_cfg("cfg0_qproj_m1_n6144_k5120", 1, 6144, 5120)
-    for m in (1, 2, 4, 8):
-        gemv_cfg(f"cfg2_down_m{m}_n5120_k17408", m, 5120, 17408)
+    if want("ns"):
+        gemv_cfg("northstar_gemv_m1_n34816_k5120", 1, 34816, 5120)
+    if want("cfg0"):
+        gemv_cfg("cfg0_qproj_m1_n6144_k5120", 1, 6144, 5120)
+    if want("cfg2"):
+        for m in (1, 2, 4, 8):
+            gemv_cfg(f"cfg2_down_m{m}_n5120_k17408", m, 5120, 17408)
 
-    # config 3: LM head + argmax (ids only, logits not stored)
-    N, K = 151936, 5120
-    rig = Rig(torch, dev, N, K, 0.01)
-    for M in (1, 8):
+    if want("cfg3"):   # LM head + argmax (ids only, logits not stored)
+        N, K = 151936, 5120
+        rig = Rig(torch, dev, N, K, 0.01)
+        for M in (1, 8):
+            X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+            ids = torch.empty(M, dtype=torch.int32, device=dev)
+            scr = torch.empty(ops.lm_head_argmax_scratch_size(M, N, K), dtype=torch.uint8, device=dev)
+            fn = lambda i: ops.lm_head_argmax_int4(ids, None, X, rig.W[i], rig.S[i], M, N, K,  # noqa
+                                                    scratch=scr)
+            w, e = time_launches(torch, fn, steps, warm, rig.copies, graph=graph)
+            b = gemv_bytes(M, N, K, 0, 0) + M * 4
+            record(f"cfg3_lmhead_argmax_m{M}", {"M": M, "N": N, "K": K, "us": round(e * 1e6, 3),
+                                                "GBps": round(b / e / 1e9, 1),
+                                                "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)})
+        del rig
+
+    if want("cfg4"):   # chunked-prefill GEMM M=512
+        M, N, K = 512, 17408, 5120
+        rig = Rig(torch, dev, N, K, 0.02)
         X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
-        ids = torch.empty(M, dtype=torch.int32, device=dev)
-        scr = torch.empty(ops.lm_head_argmax_scratch_size(M, N, K), dtype=torch.uint8, device=dev)
-        fn = lambda i: ops.lm_head_argmax_int4(ids, None, X, rig.W[i], rig.S[i], M, N, K,  # noqa
-                                                scratch=scr)
-        w, e = time_launches(torch, fn, steps, warm, rig.copies)
-        b = gemv_bytes(M, N, K, 0, 0) + M * 4
-        out[f"cfg3_lmhead_argmax_m{M}"] = {"M": M, "N": N, "K": K, "us": round(e * 1e6, 3),
-                                           "GBps": round(b / e / 1e9, 1),
-                                           "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)}
-        log(f"  cfg3 M={M}: {out[f'cfg3_lmhead_argmax_m{M}']}")
-    del rig
-
-    # config 4: chunked-prefill GEMM M=512
-    M, N, K = 512, 17408, 5120
-    rig = Rig(torch, dev, N, K, 0.02)
-    X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
-    Y = torch.empty((M, N), dtype=torch.float16, device=dev)
-    fn = lambda i: ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)  # noqa: E731
-    w, e = time_launches(torch, fn, max(5, steps // 10), 3, rig.copies)
-    fl = 2 * M * N * K
-    out["cfg4_prefill_m512_n17408_k5120"] = {"us": round(e * 1e6, 2), "TFLOPs": round(fl / e / 1e12, 1),
-                                             "frac_fp16_mfma": round(fl / e / 1e12 / FP16_PEAK_TFLOPS, 4)}
-    log(f"  cfg4: {out['cfg4_prefill_m512_n17408_k5120']}")
+        Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+        fn = lambda i: ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)  # noqa: E731
+        w, e = time_launches(torch, fn, max(32, steps // 4), 8, rig.copies, graph=graph)
+        fl = 2 * M * N * K
+        record("cfg4_prefill_m512_n17408_k5120",
+               {"M": M, "N": N, "K": K, "us": round(e * 1e6, 2), "TFLOPs": round(fl / e / 1e12, 1),
+                "frac_fp16_mfma": round(fl / e / 1e12 / FP16_PEAK_TFLOPS, 4),
+                "kernel": "xhip::gemm_int4_mfma_kernel<NQ=2,NR=1>"})
     return out
 
 
 def cpu_baseline(nbytes, log):
-    """Oracle restatement of the reference CPU loop (double accumulate), on
+    """Oracle restatement of the reference CPU loop (double accumulate) on
     the full config-1 step, repeated for >= ~10 s per thread setting."""
     try:
         import oracle
-    except Exception as e:  # the oracle library travels prebuilt; report if it is absent
+        oracle.lib()
+    except Exception as e:  # the oracle library travels prebuilt; report if absent
         log(f"cpu baseline unavailable: {e}")
         return None
     from xinfer_amd import synth

@@ -1,0 +1,170 @@
+// xinfer_hip C++ host interface: the reference's `xinfer::ops` projection
+// entry points (src/ops/linear.h, src/ops/sampling.h) with the same names,
+// overload set, argument order and meaning, implemented on the C-ABI of
+// xinfer_ops.h.  Differences from the reference signatures:
+//   * `sycl::queue&` -> `hipStream_t` (any pointer-sized stream handle works);
+//   * `sycl::half`   -> `xinfer::half` (a 16-bit IEEE binary16 storage type);
+//   * return type    -> `void`; failures throw `xinfer::ops::Error` carrying
+//     the status code (the reference returned an empty sycl::event for
+//     M, N, K <= 0 -- still a silent no-op here -- and had no error reporting).
+// Everything is asynchronous on the stream except argmax(), which, like the
+// reference (src/ops/sampling.cpp:17-92), blocks and returns the token id.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "xinfer_ops.h"
+
+typedef struct ihipStream_t* hipStream_t;
+
+namespace xinfer {
+
+struct half {
+    uint16_t bits;
+};
+
+namespace ops {
+
+struct Error : std::runtime_error {
+    int status;
+    Error(const char* fn, int st)
+        : std::runtime_error(std::string(fn) + ": " + xinfer_status_string(st)), status(st) {}
+};
+
+namespace detail {
+inline void check(const char* fn, int st) {
+    if (st != XINFER_OK) throw Error(fn, st);
+}
+inline void* q(hipStream_t s) { return reinterpret_cast<void*>(s); }
+}  // namespace detail
+
+// src/ops/linear.h:30-39  FP16 in -> FP16 out
+inline void linear_int4(hipStream_t s, half* Y, const half* X, const uint8_t* W_int4,
+                        const half* scales, const float* bias, int64_t M, int64_t N, int64_t K,
+                        int group_size = 128) {
+    detail::check("linear_int4", xinfer_linear_int4_f16(detail::q(s), Y, X, W_int4, scales, bias,
+                                                        M, N, K, group_size));
+}
+
+// src/ops/linear.h:42-51  FP16 in -> FP32 out (LM-head logits)
+inline void linear_int4(hipStream_t s, float* Y, const half* X, const uint8_t* W_int4,
+                        const half* scales, const float* bias, int64_t M, int64_t N, int64_t K,
+                        int group_size = 128) {
+    detail::check("linear_int4", xinfer_linear_int4_f16_f32out(detail::q(s), Y, X, W_int4, scales,
+                                                               bias, M, N, K, group_size));
+}
+
+// src/ops/linear.h:54-63  FP32 in -> FP32 out (oracle testing)
+inline void linear_int4(hipStream_t s, float* Y, const float* X, const uint8_t* W_int4,
+                        const half* scales, const float* bias, int64_t M, int64_t N, int64_t K,
+                        int group_size = 128) {
+    detail::check("linear_int4", xinfer_linear_int4_f32(detail::q(s), Y, X, W_int4, scales, bias,
+                                                        M, N, K, group_size));
+}
+
+// src/ops/linear.h:66-81
+struct FusedProjectionDesc {
+    half* Y{nullptr};
+    const uint8_t* W_int4{nullptr};
+    const half* scales{nullptr};
+    const float* bias{nullptr};
+    int64_t N{0};
+};
+struct FusedProjectionDescFP32 {
+    float* Y{nullptr};
+    const uint8_t* W_int4{nullptr};
+    const half* scales{nullptr};
+    const float* bias{nullptr};
+    int64_t N{0};
+};
+
+namespace detail {
+template <typename D>
+inline std::vector<xinfer_fused_desc> to_c(const D* descs, int n) {
+    std::vector<xinfer_fused_desc> v;
+    for (int i = 0; descs && i < n && i < 4; ++i)
+        v.push_back(xinfer_fused_desc{descs[i].Y, descs[i].W_int4, descs[i].scales, descs[i].bias,
+                                      descs[i].N});
+    return v;
+}
+}  // namespace detail
+
+// src/ops/linear.h:97-103
+inline void linear_int4_fused(hipStream_t s, const half* X, const FusedProjectionDesc* descs,
+                              int num_descs, int64_t M, int64_t K, int group_size = 128) {
+    auto v = detail::to_c(descs, num_descs);
+    detail::check("linear_int4_fused",
+                  xinfer_linear_int4_fused_f16(detail::q(s), X, descs ? v.data() : nullptr,
+                                               num_descs, M, K, group_size));
+}
+
+// src/ops/linear.h:105-111
+inline void linear_int4_fused(hipStream_t s, const float* X, const FusedProjectionDescFP32* descs,
+                              int num_descs, int64_t M, int64_t K, int group_size = 128) {
+    auto v = detail::to_c(descs, num_descs);
+    detail::check("linear_int4_fused",
+                  xinfer_linear_int4_fused_f32(detail::q(s), X, descs ? v.data() : nullptr,
+                                               num_descs, M, K, group_size));
+}
+
+// src/ops/linear.h:117-127
+inline void mlp_gate_up_swiglu_int4(hipStream_t s, half* Y, const half* X, const uint8_t* W_gate,
+                                    const half* scales_gate, const uint8_t* W_up,
+                                    const half* scales_up, int64_t M, int64_t N, int64_t K,
+                                    int group_size = 128) {
+    detail::check("mlp_gate_up_swiglu_int4",
+                  xinfer_mlp_gate_up_swiglu_int4_f16(detail::q(s), Y, X, W_gate, scales_gate, W_up,
+                                                     scales_up, M, N, K, group_size));
+}
+
+// src/ops/linear.h:129-139
+inline void mlp_gate_up_swiglu_int4(hipStream_t s, float* Y, const float* X, const uint8_t* W_gate,
+                                    const half* scales_gate, const uint8_t* W_up,
+                                    const half* scales_up, int64_t M, int64_t N, int64_t K,
+                                    int group_size = 128) {
+    detail::check("mlp_gate_up_swiglu_int4",
+                  xinfer_mlp_gate_up_swiglu_int4_f32(detail::q(s), Y, X, W_gate, scales_gate, W_up,
+                                                     scales_up, M, N, K, group_size));
+}
+
+// src/ops/linear.h:159-168
+inline void linear_int4_naive(hipStream_t s, float* Y, const float* X, const uint8_t* W_int4,
+                              const half* scales, const float* bias, int64_t M, int64_t N,
+                              int64_t K, int group_size = 128) {
+    detail::check("linear_int4_naive", xinfer_linear_int4_naive_f32(detail::q(s), Y, X, W_int4,
+                                                                    scales, bias, M, N, K,
+                                                                    group_size));
+}
+
+// src/ops/sampling.h:13-17 (bytes instead of an element count)
+inline size_t argmax_scratch_size(int64_t vocab_size, int64_t rows = 1) {
+    return xinfer_argmax_scratch_bytes(vocab_size, rows);
+}
+
+// Synchronous device->host copy of the id; supplied by the caller because
+// this header does not include the HIP runtime.  Returns hipSuccess (0) on
+// success.  A caller using HIP passes e.g.
+//   [](void* dst, const void* src, size_t n, hipStream_t s) {
+//       return (int)hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToHost, s) ||
+//              (int)hipStreamSynchronize(s); }
+using CopyToHostFn = int (*)(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+// src/ops/sampling.h:22-26: blocking greedy argmax -> token id.  `id_dev`
+// is an int64 slot in device memory; `scratch` may be null (library buffer)
+// or hold argmax_scratch_size(vocab_size) bytes.
+inline int64_t argmax(hipStream_t s, const float* logits, int64_t vocab_size, int64_t* id_dev,
+                      CopyToHostFn copy_to_host, void* scratch = nullptr,
+                      size_t scratch_bytes = 0) {
+    detail::check("argmax", xinfer_argmax_f32(detail::q(s), logits, vocab_size, 1, id_dev, scratch,
+                                              scratch_bytes));
+    int64_t id = 0;
+    if (copy_to_host(&id, id_dev, sizeof(id), s) != 0) throw Error("argmax", XINFER_ERR_HIP);
+    return id;
+}
+
+}  // namespace ops
+}  // namespace xinfer

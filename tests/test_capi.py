@@ -77,3 +77,19 @@ def test_scratch_sizes(L):
     assert L.xinfer_argmax_scratch_bytes(4097, 3) == 3 * 2 * 8
     assert L.xinfer_lm_head_argmax_scratch_bytes(1, 151936, 5120) > 0
     assert L.xinfer_lm_head_argmax_scratch_bytes(9, 151936, 5120) == 0
+
+
+def test_cxx_interface_compiles_links_and_validates(tmp_path):
+    """The C++ mirror of xinfer::ops builds with g++ against the C-ABI and its
+    validation paths behave (no GPU work is issued)."""
+    import subprocess
+    src = os.path.join(ROOT, "tests", "cabi_cxx_check.cpp")
+    exe = str(tmp_path / "cabi_cxx_check")
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    torch_lib = os.path.join(os.path.dirname(__import__("torch").__file__), "lib")
+    subprocess.run(["g++", "-std=c++17", "-O1", "-I", os.path.join(ROOT, "include"), src, "-o", exe,
+                    "-L", libdir, "-lxinfer_hip", f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{torch_lib}",
+                    f"-Wl,-rpath-link,{torch_lib}", "-L", torch_lib],
+                   check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "OK", (r.stdout, r.stderr)
