@@ -1,0 +1,182 @@
+"""GPU parity of the small-batch (2 <= M <= 8) decode path against the CPU
+oracle: plain / fp32-out / bias, the split-K shapes (long K, short N) whose
+k-slices are combined by the last block of each tile range, SwiGLU, fused
+descriptors and the LM-head argmax.  Same bounds as the other parity tests:
+fp16 outputs max abs <= 1e-2 and relative L2 <= 1e-3; fp32 outputs the
+reference's 1e-4 bound (tests/test_ops_oracle.cpp:781); argmax ids exact."""
+import numpy as np
+import pytest
+
+import oracle
+from tests import kat
+from tests.gpu_util import check_f16_tol, cpu_threads, f16_dev, to_dev, to_np
+from xinfer_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    import torch
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    from xinfer_amd import _lib
+    _lib.load_library()
+    yield
+    torch.cuda.synchronize()
+
+
+def _ops():
+    from xinfer_amd import ops
+    return ops
+
+
+def _empty(shape, dtype):
+    import torch
+    return torch.full(shape, float("nan"), dtype=dtype, device="cuda")
+
+
+def _inputs(seed, M, N, K, sigma=0.02):
+    W = synth.packed_weights(seed, N, K)
+    S = synth.scales(seed, N, K, sigma)
+    Xb = synth.activations(seed, M, K)
+    return W, S, Xb
+
+
+def _check_f32(y, ref):
+    err = np.abs(y - ref).max()
+    assert err <= 1e-4 * max(1.0, np.abs(ref).max()) and kat.rel_l2(y, ref) <= 1e-4, err
+    return err
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 33, 128), (8, 17, 256), (3, 1000, 1536), (8, 4096, 5120),
+                                   (6, 2000, 9984), (4, 5120, 17408), (7, 4100, 8192)])
+def test_small_batch_shapes(M, N, K):
+    import torch
+    ops = _ops()
+    print("case", M, N, K, flush=True)
+    W, S, Xb = _inputs(M * 7 + N, M, N, K)
+    dW, dS, dX = to_dev(W), f16_dev(S), f16_dev(Xb)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+    Y = _empty((M, N), torch.float16)
+    ops.linear_int4(Y, dX, dW, dS, None, M, N, K)
+    print(check_f16_tol(to_np(Y), ref))
+    Yf = _empty((M, N), torch.float32)
+    ops.linear_int4(Yf, dX, dW, dS, None, M, N, K)
+    print(_check_f32(to_np(Yf), ref))
+
+
+def test_split_k_repeatable_and_counters_reset():
+    """Long-K shapes run as several k-slices per tile range; every call must
+    give the same bits (slices are summed in slice order) and leave the
+    arrival counters ready for the next call, also across shapes."""
+    import torch
+    ops = _ops()
+    shapes = [(8, 1000, 17408), (2, 5120, 17408), (8, 1000, 17408), (5, 300, 25600)]
+    first = {}
+    for M, N, K in shapes:
+        print("case", M, N, K, flush=True)
+        W, S, Xb = _inputs(N + K, M, N, K)
+        dW, dS, dX = to_dev(W), f16_dev(S), f16_dev(Xb)
+        ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+        outs = []
+        for _ in range(3):
+            Y = _empty((M, N), torch.float32)
+            ops.linear_int4(Y, dX, dW, dS, None, M, N, K)
+            outs.append(to_np(Y))
+        for y in outs[1:]:
+            assert np.array_equal(y.view(np.uint32), outs[0].view(np.uint32))
+        _check_f32(outs[0], ref)
+        key = (M, N, K)
+        if key in first:
+            assert np.array_equal(first[key].view(np.uint32), outs[0].view(np.uint32))
+        first[key] = outs[0]
+
+
+def test_small_batch_bias_f32():
+    import torch
+    ops = _ops()
+    M, N, K = 4, 777, 4096
+    W, S, Xb = _inputs(12, M, N, K)
+    bias = np.linspace(-3, 3, N).astype(np.float32)
+    for K_ in (K, 17408):
+        W, S, Xb = _inputs(12, M, N, K_)
+        ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K_, bias=bias, nthreads=cpu_threads())
+        Y = _empty((M, N), torch.float32)
+        ops.linear_int4(Y, f16_dev(Xb), to_dev(W), f16_dev(S), to_dev(bias), M, N, K_)
+        _check_f32(to_np(Y), ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(2, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (5, 640, 17408)])
+def test_small_batch_swiglu(M, N, K):
+    import torch
+    ops = _ops()
+    print("case", M, N, K, flush=True)
+    Wg, Wu = synth.packed_weights(3, N, K), synth.packed_weights(3, N, K, synth.STREAM_W2)
+    Sg, Su = synth.scales(3, N, K), synth.scales(3, N, K, stream=synth.STREAM_S2)
+    Xb = synth.activations(3, M, K)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), to_dev(Wg), f16_dev(Sg), to_dev(Wu), f16_dev(Su),
+                                M, N, K)
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb), Wg, Sg, Wu, Su, M, N, K, nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y), ref))
+
+
+@pytest.mark.parametrize("M", [2, 3, 8])
+def test_small_batch_fused_descs(M):
+    import torch
+    ops = _ops()
+    K, Ns = 2048, (384, 128, 64, 40)
+    Xb = synth.activations(20 + M, M, K)
+    X = oracle.f16_to_f32(Xb)
+    descs, refs, outs = [], [], []
+    for p, N in enumerate(Ns):
+        W, S = synth.packed_weights(30 + p, N, K), synth.scales(30 + p, N, K)
+        bias = np.linspace(-1, 1, N).astype(np.float32) if p == 1 else None
+        refs.append(oracle.linear_int4(X, W, S, M, N, K, bias=bias))
+        Y = _empty((M, N), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S),
+                                             None if bias is None else to_dev(bias), N))
+    ops.linear_int4_fused(f16_dev(Xb), descs, 4, M, K)
+    for Y, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Y), ref))
+
+
+@pytest.mark.parametrize("M", [2, 4, 7])
+def test_small_batch_lm_head_argmax(M):
+    import torch
+    ops = _ops()
+    N, K = 50021, 5120
+    W, S, Xb = _inputs(40 + M, M, N, K, 0.01)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    logits = _empty((M, N), torch.float32)
+    ops.lm_head_argmax_int4(ids, logits, f16_dev(Xb), to_dev(W), f16_dev(S), M, N, K)
+    got, lg = to_np(ids), to_np(logits)
+    for m in range(M):
+        print("row", m, "id", got[m], "margin", oracle.top2_margin(ref[m]))
+        assert got[m] == oracle.argmax(ref[m]) == oracle.argmax(lg[m])
+    _check_f32(lg, ref)
+
+
+def test_small_batch_lm_head_ties_lowest_index():
+    import torch
+    ops = _ops()
+    M, N, K = 3, 4096, 512
+    W, S, Xb = _inputs(2, M, N, K)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K)
+    want = []
+    for m in range(M):
+        b = int(np.argmax(ref[m]))
+        dups = [(b + 1000 * (m + 1)) % N, (b + 2999) % N]
+        for dst in dups:
+            W[dst] = W[b]
+            S[dst] = S[b]
+        want.append(b)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    ops.lm_head_argmax_int4(ids, None, f16_dev(Xb), to_dev(W), f16_dev(S), M, N, K)
+    got = to_np(ids)
+    for m in range(M):
+        assert got[m] == oracle.argmax(ref[m])

@@ -180,8 +180,9 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
         const uint32_t row0 = (uint32_t)(row_begin + lg * G2);   // first row of the item
         const bool lane_bad = (ragged && ls == nsteps - 1 && l32 >= ragged) || lcount <= 0;
         --lcount;
-        const uint32_t wv = lane_bad ? 0x80000000u : w_lane + row0 * row_bytes + (uint32_t)ls * 512u;
-        const uint32_t sv = lane_bad ? 0x80000000u : s_lane + row0 * srow_bytes + (uint32_t)ls * 16u;
+        // 0xFFFFF000 lies past every resource (matrices are < 4 GiB - 4096)
+        const uint32_t wv = lane_bad ? 0xFFFFF000u : w_lane + row0 * row_bytes + (uint32_t)ls * 512u;
+        const uint32_t sv = lane_bad ? 0xFFFFF000u : s_lane + row0 * srow_bytes + (uint32_t)ls * 16u;
 #pragma unroll
         for (int r = 0; r < RR; ++r) {
             const int rr = (EPI == EPI_SWIGLU) ? (r % R) : r;
@@ -658,8 +659,17 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
 
 }  // namespace xhip_host
 
-// Forward declaration: M > 8 with fp16 activations (chunked prefill).
+// Forward declarations: M > 8 with fp16 activations (chunked prefill) and
+// the MFMA small-batch kernel for 2 <= M <= 8 (gemv_mb_int4.hip; each returns
+// 1 when the shape is left to the VALU GEMV here).
 namespace xhip_host {
+int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
+              int64_t M, int64_t K, int* rc);
+int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
+              const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K, int* rc);
+int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts);
+int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
+              int64_t M, int64_t N, int64_t K, ArgCand* parts, int* nparts, int* rc);
 int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
                   const uint16_t* S, const uint8_t* W2, const uint16_t* S2, const float* bias,
                   int64_t M, int64_t N, int64_t K);
@@ -681,6 +691,11 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (M > 8)
         return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K);
+    if (M >= 2) {
+        const xinfer_fused_desc one = {Y, W, S, bias, N};
+        int mrc = XINFER_OK;
+        if (!mb_linear(st, &one, 1, X, y_f32, M, K, &mrc)) return mrc;
+    }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);
@@ -720,6 +735,7 @@ int xinfer_linear_int4_fused_f16(void* stream, const void* X, const xinfer_fused
     GemvParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
+    xinfer_fused_desc live[4];
     int nd = 0;
     for (int i = 0; i < num_descs; ++i) {
         const xinfer_fused_desc& q = descs[i];
@@ -735,6 +751,7 @@ int xinfer_linear_int4_fused_f16(void* stream, const void* X, const xinfer_fused
             if (rc) return rc;
             continue;
         }
+        live[nd] = q;
         GemvDesc& g = p.d[nd++];
         g.W = q.W_int4;
         g.S = reinterpret_cast<const uint16_t*>(q.scales);
@@ -743,6 +760,10 @@ int xinfer_linear_int4_fused_f16(void* stream, const void* X, const xinfer_fused
         g.N = (int32_t)q.N;
     }
     if (M > 8 || nd == 0) return XINFER_OK;
+    if (M >= 2) {
+        int mrc = XINFER_OK;
+        if (!mb_linear(st, live, nd, X, false, M, K, &mrc)) return mrc;
+    }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);
 }
@@ -763,6 +784,10 @@ int xinfer_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
     if (M > 8)
         return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
                              (const uint16_t*)scales_up, nullptr, M, N, K);
+    if (M >= 2) {
+        int mrc = XINFER_OK;
+        if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc)) return mrc;
+    }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);
@@ -778,6 +803,9 @@ int xinfer_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
 
 size_t xinfer_lm_head_argmax_scratch_bytes(int64_t M, int64_t N, int64_t K) {
     if (M <= 0 || N <= 0 || M > 8) return 0;
+    int nparts = 0;
+    if (M >= 2 && K > 0 && !xhip_host::mb_argmax_plan(M, N, K, &nparts))
+        return (size_t)M * (size_t)nparts * sizeof(ArgCand);
     GemvParams p = {};
     p.ndesc = 1;
     p.K = (int32_t)(K > 0 ? K : 128);
@@ -807,6 +835,24 @@ extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* log
         !aligned(ids, 4))
         return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    int nparts = 0;
+    if (M >= 2 && !mb_argmax_plan(M, N, K, &nparts)) {
+        const size_t need = (size_t)M * (size_t)nparts * sizeof(ArgCand);
+        if (!scratch) {
+            scratch = library_scratch(need);
+            if (!scratch) return XINFER_ERR_SCRATCH;
+        } else if (scratch_bytes < need || !aligned(scratch, 8)) {
+            return XINFER_ERR_SCRATCH;
+        }
+        ArgCand* parts = reinterpret_cast<ArgCand*>(scratch);
+        int mrc = XINFER_OK;
+        if (!mb_argmax(st, logits, X, W_int4, scales, M, N, K, parts, &nparts, &mrc)) {
+            if (mrc) return mrc;
+            hipLaunchKernelGGL((argmax_finalize_kernel<int32_t>), dim3((unsigned)M), dim3(256), 0, st,
+                               parts, (int32_t)nparts, ids);
+            return launch_status();
+        }
+    }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);

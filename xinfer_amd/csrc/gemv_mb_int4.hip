@@ -1,0 +1,658 @@
+// INT4-G128-SYM small-batch decode projection (2 <= M <= 8) on gfx950.
+//
+// Same contract as the reference's sub-group GEMV at M > 1 (the batched rows
+// of src/ops/linear.cpp:165-305, the fused variants 351-498 and 501-617, and
+// the LM-head linear + argmax of src/targets/qwen3_8/forward.cpp:304-307):
+// every output is sum_k x[m][k] * q[n][k] * s[n][k/128] with FP32
+// accumulation.  At M = 8 a dot-product GEMV spends 4 * M v_dot2 per packed
+// dword on top of its decode: more VALU time than the HBM stream it rides
+// on.  This kernel decodes each nibble once and lets the matrix cores apply
+// it to all M rows:
+//
+//   * output tile = 16 weight rows (n) x 16 activation rows (m, the first M
+//     real).  Per 128-k group a lane loads one 16-byte chunk of packed
+//     weights: lane l holds row n = l % 16 and k-quarter l / 16 of the group,
+//     which is exactly the B-operand layout of v_mfma_f32_16x16x32_f16.  The
+//     nibbles are decoded to exact fp16 integers (dequant8: one v_bitop3_b32
+//     and one packed add/fma per pair) and fed to four MFMAs (one per dword)
+//     that sum the whole group in FP32; the group's fp16 scale is then applied
+//     to the group sum in FP32 (acc += s * sum), as in the reference.
+//   * the A operand (activations) comes from LDS: the block stages its k-slice
+//     of X once, permuted into the pair order of the decode, so that lane l
+//     (row m = l % 16, k-quarter l / 16) reads one ds_read_b128 per MFMA.
+//     Rows m >= M read row M - 1: they only feed output rows that are dropped.
+//   * a block owns a contiguous range of 16-row tiles and one k-slice; its
+//     waves take contiguous runs of tiles, T at a time, and stream every
+//     group of the slice with the next PF items in flight (raw buffer loads,
+//     branch-free: rows past N and padding items read zeros without memory
+//     traffic).  Results go through LDS to a coalesced epilogue.
+//   * when K is long and N short (the down projection) the planner splits K
+//     over ks blocks per tile range.  Each writes its FP32 partial sums to a
+//     workspace; the last block of a range (device-scope counter) adds the
+//     slices in slice order, so results do not depend on timing, and resets
+//     the counter for the next call.
+// Epilogues: bias + fp16/fp32 store, SiLU(gate) * up (paired tiles), and the
+// LM-head argmax (per-block candidates, reduced by argmax_finalize_kernel).
+
+#include <stdlib.h>
+
+#include <mutex>
+
+#include "common.h"
+
+namespace xhip {
+
+enum MbEpilogue { MB_PLAIN = 0, MB_SWIGLU = 1, MB_ARGMAX = 2 };
+
+struct MbDesc {
+    const uint8_t* W;    // [N][K/2]   (gate matrix for MB_SWIGLU)
+    const uint16_t* S;   // [N][K/128]
+    const uint8_t* W2;   // up matrix (MB_SWIGLU only)
+    const uint16_t* S2;
+    const float* bias;   // optional [N]
+    void* Y;             // [M][N] output (MB_ARGMAX: optional fp32 logits)
+    int32_t N;
+    int32_t block_begin; // first block of this descriptor
+    int32_t range_begin; // first tile range of this descriptor (counters, parts)
+    int32_t pad;
+};
+
+struct MbParams {
+    MbDesc d[4];
+    const f16* X;        // [M][K]
+    ArgCand* parts;      // MB_ARGMAX: [M][nranges] block candidates
+    float* ws;           // ks > 1: [ks][E][M][N] partial sums, slices ws_slice floats apart
+    uint32_t* cnt;       // ks > 1: one arrival counter per tile range (zero between calls)
+    int64_t ws_desc[4];  // float offset of each descriptor's partials in ws
+    int32_t ws_slice[4]; // floats per k-slice of each descriptor (multiple of 64: 256-byte aligned)
+    int32_t ndesc;
+    int32_t M;           // 2..8
+    int32_t K;
+    int32_t ks;          // k-slices per tile range
+    int32_t gps;         // groups per k-slice (the last slice may be shorter)
+    int32_t tiles_blk;   // 16-row tiles per block
+    int32_t nranges;     // tile ranges over all descriptors
+    int32_t pad;
+};
+
+constexpr uint32_t kOutOfRange = 0xFFFFF000u;  // >= every buffer resource size used here
+
+// Two groups per item: a lane's two 16-byte loads of an item fall in the same
+// 128-byte line of its row.  Weights are loaded with the default cache policy
+// (measured faster here than the streaming hint: the other half of each line
+// is read by the same wave a few instructions later).
+#ifndef XHIP_MB_GP
+#define XHIP_MB_GP 2
+#endif
+#ifndef XHIP_MB_AUX
+#define XHIP_MB_AUX 0
+#endif
+constexpr int kGP = XHIP_MB_GP;  // 128-k groups per item
+// Cache-policy bit for device-scope coherence (sc1): stores write through and
+// loads do not hit stale lines of another XCD's L2.
+constexpr int kDeviceCoherent = 16;
+
+template <int TT>
+struct MbItem {
+    u32x4 w[TT * kGP];
+    uint32_t s[TT * kGP];  // raw fp16 scale bits, converted at use
+};
+
+__device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
+    f16x8 r;
+    r[0] = q[0].x; r[1] = q[0].y; r[2] = q[1].x; r[3] = q[1].y;
+    r[4] = q[2].x; r[5] = q[2].y; r[6] = q[3].x; r[7] = q[3].y;
+    return r;
+}
+
+template <int T, int EPI, typename OutT, int NW, int PF>
+__global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p) {
+    constexpr int E = (EPI == MB_SWIGLU) ? 2 : 1;  // sums per output
+    constexpr int TT = T * E;                      // weight tiles per item
+    constexpr int NT = 64 * NW;
+
+    extern __shared__ __align__(16) unsigned char smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int l16 = lane & 15;
+    const int kq = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+
+    int di = 0;
+#pragma unroll
+    for (int i = 1; i < 4; ++i)
+        if (i < p.ndesc && (int)blockIdx.x >= p.d[i].block_begin) di = i;
+    const MbDesc& d = p.d[di];
+    const int N = d.N;
+    const int K = p.K;
+    const int M = p.M;
+    const int ks = p.ks;
+    const int local = (int)blockIdx.x - d.block_begin;
+    const int range = local / ks;
+    const int slice = local - range * ks;
+    const int grange = d.range_begin + range;
+    const int n0 = range * p.tiles_blk * 16;
+    const int rows_here = min(p.tiles_blk * 16, N - n0);
+    const int tiles_here = (rows_here + 15) >> 4;
+    const int ng = K >> 7;
+    const int g0 = slice * p.gps;
+    const int ngs = min(p.gps, ng - g0);
+    const uint32_t row_bytes = (uint32_t)K >> 1;
+
+    // LDS: X slice as MFMA A operands [group][dword t][k-quarter][m] (16 B
+    // each), then the block's results [row][m][e] (fp32), then the argmax
+    // candidates of the waves (NW values, NW indices) and one flag word.
+    f16x8* xs = reinterpret_cast<f16x8*>(smem);
+    float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * M * 16);
+    float* candv = outl + (size_t)p.tiles_blk * 16 * M * E;
+    int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
+    int32_t* flag = candi + NW;
+
+    // stage X[:, slice] (permuted to the decode's pair order)
+    {
+        const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
+        for (int i = tid; i < chunks; i += NT) {
+            const int m = i % M;
+            const int q = i / M;
+            const int cq = q & 3, gl = q >> 2;
+            const u32x4* src = reinterpret_cast<const u32x4*>(p.X + (size_t)m * K + (size_t)(g0 + gl) * 128 + cq * 32);
+            u32x4 xv[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xv[v] = src[v];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t xa[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+                f16x2 pr[4];
+                permute_x8(xa, pr);
+                xs[((gl * 4 + t) * 4 + cq) * M + m] = pack_q8(pr);
+            }
+        }
+    }
+
+    // this wave's run of tiles, processed T at a time (the last chunk may be
+    // partial: its missing tiles load nothing and are never stored)
+    const int t0 = (wave * tiles_here) / NW;
+    const int t1 = ((wave + 1) * tiles_here) / NW;
+    const int nchunks = (t1 - t0 + T - 1) / T;
+    const int nig = (ngs + kGP - 1) / kGP;  // items per chunk
+    const int nreal = nchunks * nig;
+
+    const uint32_t srow_bytes = (uint32_t)ng * 2u;
+    const int nrec_w = (int)((uint32_t)N * row_bytes);
+    const int nrec_s = (int)((uint32_t)N * srow_bytes);
+    const __amdgpu_buffer_rsrc_t rw0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.W, (short)0, nrec_w, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.S, (short)0, nrec_s, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(EPI == MB_SWIGLU ? d.W2 : d.W), (short)0, nrec_w, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(EPI == MB_SWIGLU ? d.S2 : d.S), (short)0, nrec_s, 0x00020000);
+
+    // load cursor: (chunk, group in slice) of the next item; wave-uniform
+    int lc = 0, lgl = 0, lcount = nreal;
+    auto load_next = [&](MbItem<TT>& b) {
+        const bool item_ok = lcount > 0;
+        --lcount;
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            const int tile = t0 + lc * T + j;
+            const int n = n0 + tile * 16 + l16;
+            const bool ok = item_ok && tile < t1 && n < N;
+#pragma unroll
+            for (int gi = 0; gi < kGP; ++gi) {
+                const int gl = lgl * kGP + gi;
+                const bool okg = ok && (kGP == 1 || gl < ngs);
+                const uint32_t wo = okg ? (uint32_t)n * row_bytes + (uint32_t)(g0 + gl) * 64u + (uint32_t)kq * 16u
+                                        : kOutOfRange;
+                const uint32_t so = okg ? ((uint32_t)n * (uint32_t)ng + (uint32_t)(g0 + gl)) * 2u : kOutOfRange;
+#pragma unroll
+                for (int e = 0; e < E; ++e) {
+                    b.w[(j * E + e) * kGP + gi] =
+                        __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)wo, 0, XHIP_MB_AUX);
+                    b.s[(j * E + e) * kGP + gi] = __builtin_amdgcn_raw_buffer_load_b16(e ? rs1 : rs0, (int)so, 0, 0);
+                }
+            }
+        }
+        if (++lgl == nig) { lgl = 0; ++lc; }
+    };
+
+    MbItem<TT> buf[PF + 1];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) load_next(buf[j]);
+
+    __syncthreads();  // X staged
+
+    f32x4 acc[TT];
+#pragma unroll
+    for (int j = 0; j < TT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const int mm = l16 < M ? l16 : M - 1;
+    auto compute_item = [&](int it, const MbItem<TT>& b) {
+#pragma unroll
+        for (int gi = 0; gi < kGP; ++gi) {
+            const int gl = min(it * kGP + gi, ngs - 1);  // a padding group has w = 0
+            f16x8 xa[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xa[t] = xs[((gl * 4 + t) * 4 + kq) * M + mm];
+#pragma unroll
+            for (int j = 0; j < TT; ++j) {
+                const u32x4 wv = b.w[j * kGP + gi];
+                const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+                f32x4 c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    f16x2 q[4];
+                    dequant8(wd[t], q);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[t], pack_q8(q), c, 0, 0, 0);
+                }
+                const float s = h2f((uint16_t)b.s[j * kGP + gi]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[j][e] = __builtin_fmaf(s, c[e], acc[j][e]);
+            }
+        }
+    };
+
+    // D layout of the 16x16 MFMA: lane l holds rows m = 4 * (l / 16) + e
+    // (e = 0..3) of column n = l % 16.
+    auto flush = [&](int c) {
+#pragma unroll
+        for (int j = 0; j < T; ++j) {
+            const int tile = t0 + c * T + j;
+            if (tile < t1) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 4 * kq + e;
+                    if (m < M) {
+#pragma unroll
+                        for (int x = 0; x < E; ++x)
+                            outl[((tile * 16 + l16) * M + m) * E + x] = acc[j * E + x][e];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    };
+
+    int cc = 0, cgl = 0;
+    for (int base = 0; base < nreal; base += PF + 1) {
+#pragma unroll
+        for (int j = 0; j <= PF; ++j) {
+            load_next(buf[(j + PF) % (PF + 1)]);
+            compute_item(min(cgl, nig - 1), buf[j]);
+            if (base + j < nreal && ++cgl == nig) {
+                flush(cc);
+                cgl = 0;
+                ++cc;
+            }
+        }
+    }
+    __syncthreads();
+
+    // ---- epilogue over the block's rows x M (n fastest: coalesced stores)
+    const int nout = rows_here * M;
+    if (ks > 1) {
+        // partials [slice][e][m][n] of this descriptor (< 2 GiB: checked on the host)
+        const uint32_t sst = (uint32_t)p.ws_slice[di];
+        const __amdgpu_buffer_rsrc_t rws = __builtin_amdgcn_make_buffer_rsrc(
+            p.ws + p.ws_desc[di], (short)0, (int)((uint32_t)ks * sst * 4u), 0x00020000);
+        for (int o = tid; o < nout; o += NT) {
+            const int m = o / rows_here, rl = o - m * rows_here;
+#pragma unroll
+            for (int x = 0; x < E; ++x)
+                __builtin_amdgcn_raw_buffer_store_b32(
+                    __builtin_bit_cast(uint32_t, outl[(rl * M + m) * E + x]), rws,
+                    (int)(((uint32_t)slice * sst + ((uint32_t)x * M + m) * (uint32_t)N + n0 + rl) * 4u), 0,
+                    kDeviceCoherent);
+        }
+        // Device-coherent stores and loads keep the partials consistent across
+        // the XCDs' L2s without a device-wide fence (which would write back and
+        // invalidate every L2 once per block).  The barrier waits for this
+        // block's stores to complete before the arrival is counted.
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t old = __hip_atomic_fetch_add(&p.cnt[grange], 1u, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+            flag[0] = (old == (uint32_t)(ks - 1)) ? 1 : 0;
+        }
+        __syncthreads();
+        if (flag[0] == 0) return;  // another slice of this range finishes it
+        // acquire: drop lines of this XCD's L2 that may hold stale partials
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        for (int o = tid; o < nout; o += NT) {
+            const int m = o / rows_here, rl = o - m * rows_here;
+#pragma unroll
+            for (int x = 0; x < E; ++x) {
+                float v = 0.0f;
+                for (int s = 0; s < ks; ++s)
+                    v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                        rws, (int)(((uint32_t)s * sst + ((uint32_t)x * M + m) * (uint32_t)N + n0 + rl) * 4u), 0,
+                        kDeviceCoherent));
+                outl[(rl * M + m) * E + x] = v;
+            }
+        }
+        __syncthreads();
+        if (tid == 0) __hip_atomic_store(&p.cnt[grange], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+
+    if (EPI == MB_ARGMAX) {
+        for (int m = 0; m < M; ++m) {
+            float bv = -__builtin_inff();
+            int32_t bi = 0x7FFFFFFF;
+            for (int rl = tid; rl < rows_here; rl += NT) {
+                const int n = n0 + rl;
+                float v = outl[rl * M + m];
+                if (d.bias) v += d.bias[n];
+                if (d.Y) reinterpret_cast<float*>(d.Y)[(size_t)m * N + n] = v;
+                const float key = argmax_key(v, n);
+                if (arg_better(key, n, bv, bi)) { bv = key; bi = n; }
+            }
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) {
+                const float ov = __shfl_xor(bv, off);
+                const int32_t oi = __shfl_xor(bi, off);
+                if (arg_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            }
+            if (lane == 0) {
+                candv[wave] = bv;
+                candi[wave] = bi;
+            }
+            __syncthreads();
+            if (tid == 0) {
+                float b = candv[0];
+                int32_t i = candi[0];
+                for (int w = 1; w < NW; ++w)
+                    if (arg_better(candv[w], candi[w], b, i)) { b = candv[w]; i = candi[w]; }
+                ArgCand c;
+                c.v = b;
+                c.i = i;
+                p.parts[(size_t)m * p.nranges + grange] = c;
+            }
+            __syncthreads();
+        }
+    } else {
+        for (int o = tid; o < nout; o += NT) {
+            const int m = o / rows_here, rl = o - m * rows_here;
+            const int n = n0 + rl;
+            float v = outl[(rl * M + m) * E];
+            if (EPI == MB_SWIGLU) {
+                const float u = outl[(rl * M + m) * E + 1];
+                v = v / (1.0f + expf(-v)) * u;
+            } else if (d.bias) {
+                v += d.bias[n];
+            }
+            reinterpret_cast<OutT*>(d.Y)[(size_t)m * N + n] = (OutT)v;
+        }
+    }
+}
+
+}  // namespace xhip
+
+// ------------------------------------------------------------------ host ----
+
+using namespace xhip;
+
+namespace {
+
+typedef void (*MbKernel)(MbParams);
+
+template <int T, int EPI, typename OutT>
+MbKernel mb_pick_nw(int nw) {
+    return nw >= 16 ? gemv_mb_int4_kernel<T, EPI, OutT, 16, 3>
+         : nw >= 8  ? gemv_mb_int4_kernel<T, EPI, OutT, 8, 3>
+                    : gemv_mb_int4_kernel<T, EPI, OutT, 4, 3>;
+}
+
+template <int EPI, typename OutT>
+MbKernel mb_kernel_for(int t, int nw) {
+    return t >= 2 ? mb_pick_nw<2, EPI, OutT>(nw) : mb_pick_nw<1, EPI, OutT>(nw);
+}
+
+int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return (v && *v) ? atoi(v) : dflt;
+}
+
+struct MbOverrides {
+    int t, nw, ks, bpc, min_m;
+};
+const MbOverrides& mb_overrides() {
+    static const MbOverrides o = {env_int("XINFER_MB_T", 0), env_int("XINFER_MB_NW", 0),
+                                  env_int("XINFER_MB_KS", 0), env_int("XINFER_MB_BPC", 0),
+                                  env_int("XINFER_MB_MIN_M", 0)};
+    return o;
+}
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+// Per-device workspace for split-K partial sums plus a zeroed counter array.
+// Grown on demand (outside any graph capture: the first call of a shape
+// allocates), never freed; counters are reset by the kernels themselves.
+constexpr size_t kMaxRanges = 1 << 16;
+bool mb_workspace(size_t ws_bytes, float** ws, uint32_t** cnt) {
+    static std::mutex mu;
+    static void* wbuf[64] = {nullptr};
+    static size_t wcap[64] = {0};
+    static uint32_t* cbuf[64] = {nullptr};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+    std::lock_guard<std::mutex> lock(mu);
+    if (!cbuf[dev]) {
+        void* c = nullptr;
+        if (hipMalloc(&c, kMaxRanges * sizeof(uint32_t)) != hipSuccess) return false;
+        if (hipMemset(c, 0, kMaxRanges * sizeof(uint32_t)) != hipSuccess) return false;
+        if (hipDeviceSynchronize() != hipSuccess) return false;
+        cbuf[dev] = reinterpret_cast<uint32_t*>(c);
+    }
+    if (wcap[dev] < ws_bytes) {
+        const size_t want = ws_bytes < (4u << 20) ? (4u << 20) : ws_bytes;
+        void* w = nullptr;
+        if (hipMalloc(&w, want) != hipSuccess) return false;
+        wbuf[dev] = w;  // the previous buffer may still be read by queued work: kept
+        wcap[dev] = want;
+    }
+    *ws = reinterpret_cast<float*>(wbuf[dev]);
+    *cnt = cbuf[dev];
+    return true;
+}
+
+}  // namespace
+
+namespace xhip_host {
+
+struct MbPlan {
+    int t, nw, ks, gps, tiles_blk, blocks, nranges;
+    size_t lds, ws_floats;
+    MbKernel k;
+};
+
+// Plan a small-batch launch.  Returns false when the shape does not fit the
+// kernel (X slice of one group per block beyond LDS) or M is outside 2..8.
+//   ks:  the smallest number of k-slices whose X slice fits the LDS budget,
+//        raised while the tile ranges alone cannot give every CU `bpc`
+//        blocks (short N, long K); argmax keeps ks = 1.
+//   tiles per block: the tiles spread evenly over cus * bpc / ks ranges,
+//        at least one per wave.
+//   T:   tiles per wave item (1 unless overridden).
+template <int EPI, typename OutT>
+bool plan_mb(MbParams& p, MbPlan& pl) {
+    const MbOverrides& ov = mb_overrides();
+    const int M = p.M;
+    const int min_m = ov.min_m > 0 ? ov.min_m : 3;  // M = 2: the VALU GEMV measured faster
+    if (M < min_m || M < 2 || M > 8) return false;
+    const int E = EPI == MB_SWIGLU ? 2 : 1;
+    const int ng = p.K / 128;
+    const int cus = num_cus();
+    int64_t tiles_total = 0;
+    for (int i = 0; i < p.ndesc; ++i) tiles_total += (p.d[i].N + 15) / 16;
+    const size_t xg = (size_t)M * 256;  // LDS bytes of X per group
+    const size_t x_budget = EPI == MB_ARGMAX ? 96 * 1024 : 48 * 1024;
+    int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
+    if (EPI == MB_ARGMAX) ks = 1;
+    if (ks > ng) ks = ng;
+    int nw = ov.nw > 0 ? ov.nw : ((size_t)ng * xg / ks > 64 * 1024 ? 8 : 4);
+    nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
+    const int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
+    const int64_t target = (int64_t)cus * bpc;
+    int64_t tiles_blk = 0, ranges = 0;
+    for (int pass = 0; pass < 2; ++pass) {
+        int64_t rt = target / ks;
+        if (rt < 1) rt = 1;
+        tiles_blk = (tiles_total + rt - 1) / rt;
+        if (tiles_blk < nw) tiles_blk = nw;
+        ranges = 0;
+        for (int i = 0; i < p.ndesc; ++i) ranges += ((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk;
+        if (pass == 0 && ov.ks <= 0 && EPI != MB_ARGMAX && ranges * ks < target) {
+            int ks2 = (int)(target / ranges);
+            if (ks2 > ng) ks2 = ng;
+            if (ks2 > ks) { ks = ks2; continue; }
+        }
+        break;
+    }
+    const int gps = (ng + ks - 1) / ks;
+    ks = (ng + gps - 1) / gps;
+    const int per_wave = (int)((tiles_blk + nw - 1) / nw);
+    (void)per_wave;
+    // T = 1 measured fastest on every MI355X shape tried (waves own 1-5 tiles;
+    // a partial last chunk of T > 1 costs decode and MFMA work)
+    int t = ov.t > 0 ? ov.t : 1;
+    t = t >= 2 ? 2 : 1;
+    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 + 2 * nw * 4 + 16;
+    if (lds > kMaxLds) return false;
+    if (ks > 1 && ranges > (int64_t)kMaxRanges) return false;
+    for (int i = 0; ks > 1 && i < p.ndesc; ++i)  // 32-bit buffer offsets into the partials
+        if ((int64_t)ks * (E * M * p.d[i].N + 64) * 4 >= (1LL << 31)) return false;
+    pl.t = t;
+    pl.nw = nw;
+    pl.ks = ks;
+    pl.gps = gps;
+    pl.tiles_blk = (int)tiles_blk;
+    pl.nranges = (int)ranges;
+    pl.lds = lds;
+    pl.k = mb_kernel_for<EPI, OutT>(t, nw);
+    int blocks = 0, rbeg = 0;
+    int64_t wsoff = 0;
+    for (int i = 0; i < p.ndesc; ++i) {
+        const int r = (int)(((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk);
+        p.d[i].block_begin = blocks;
+        p.d[i].range_begin = rbeg;
+        p.ws_desc[i] = wsoff;
+        p.ws_slice[i] = (int32_t)(((int64_t)E * M * p.d[i].N + 63) / 64 * 64);
+        blocks += r * ks;
+        rbeg += r;
+        wsoff += (int64_t)ks * p.ws_slice[i];
+    }
+    for (int i = p.ndesc; i < 4; ++i) {
+        p.d[i] = p.d[0];
+        p.d[i].block_begin = 0x7FFFFFFF;
+        p.ws_desc[i] = 0;
+        p.ws_slice[i] = 0;
+    }
+    pl.blocks = blocks;
+    pl.ws_floats = ks > 1 ? (size_t)wsoff : 0;
+    p.ks = ks;
+    p.gps = gps;
+    p.tiles_blk = (int)tiles_blk;
+    p.nranges = (int)ranges;
+    return true;
+}
+
+template <int EPI, typename OutT>
+int launch_mb(const MbParams& p0, const MbPlan& pl, hipStream_t st) {
+    MbParams p = p0;
+    if (pl.ks > 1) {
+        if (!mb_workspace(pl.ws_floats * sizeof(float), &p.ws, &p.cnt)) return XINFER_ERR_SCRATCH;
+    }
+    if (pl.lds > 64 * 1024) {
+        static std::mutex mu;
+        static const void* done[256];
+        static int ndone = 0;
+        std::lock_guard<std::mutex> lock(mu);
+        bool seen = false;
+        for (int i = 0; i < ndone; ++i) seen |= done[i] == reinterpret_cast<const void*>(pl.k);
+        if (!seen) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(pl.k),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)kMaxLds) != hipSuccess)
+                return XINFER_ERR_HIP;
+            if (ndone < 256) done[ndone++] = reinterpret_cast<const void*>(pl.k);
+        }
+    }
+    hipLaunchKernelGGL(pl.k, dim3((unsigned)pl.blocks), dim3(64 * pl.nw), pl.lds, st, p);
+    return launch_status();
+}
+
+// Entry points used by the GEMV front end (gemv_int4.hip).  Return 1 when the
+// shape is not handled here (the caller then runs the VALU GEMV).
+int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
+              int64_t M, int64_t K, int* rc) {
+    MbParams p = {};
+    p.X = reinterpret_cast<const f16*>(X);
+    p.M = (int32_t)M;
+    p.K = (int32_t)K;
+    p.ndesc = nd;
+    for (int i = 0; i < nd; ++i) {
+        p.d[i].W = descs[i].W_int4;
+        p.d[i].S = reinterpret_cast<const uint16_t*>(descs[i].scales);
+        p.d[i].bias = descs[i].bias;
+        p.d[i].Y = descs[i].Y;
+        p.d[i].N = (int32_t)descs[i].N;
+    }
+    MbPlan pl;
+    const bool ok = y_f32 ? plan_mb<MB_PLAIN, float>(p, pl) : plan_mb<MB_PLAIN, f16>(p, pl);
+    if (!ok) return 1;
+    *rc = y_f32 ? launch_mb<MB_PLAIN, float>(p, pl, st) : launch_mb<MB_PLAIN, f16>(p, pl, st);
+    return 0;
+}
+
+int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
+              const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K, int* rc) {
+    MbParams p = {};
+    p.X = reinterpret_cast<const f16*>(X);
+    p.M = (int32_t)M;
+    p.K = (int32_t)K;
+    p.ndesc = 1;
+    p.d[0].W = Wg;
+    p.d[0].S = reinterpret_cast<const uint16_t*>(Sg);
+    p.d[0].W2 = Wu;
+    p.d[0].S2 = reinterpret_cast<const uint16_t*>(Su);
+    p.d[0].Y = Y;
+    p.d[0].N = (int32_t)N;
+    MbPlan pl;
+    if (!plan_mb<MB_SWIGLU, f16>(p, pl)) return 1;
+    *rc = launch_mb<MB_SWIGLU, f16>(p, pl, st);
+    return 0;
+}
+
+// LM head: plan only (nranges = candidate count per row), or plan + launch.
+int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts) {
+    MbParams p = {};
+    p.M = (int32_t)M;
+    p.K = (int32_t)K;
+    p.ndesc = 1;
+    p.d[0].N = (int32_t)N;
+    MbPlan pl;
+    if (!plan_mb<MB_ARGMAX, float>(p, pl)) return 1;
+    *nparts = pl.nranges;
+    return 0;
+}
+
+int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
+              int64_t M, int64_t N, int64_t K, ArgCand* parts, int* nparts, int* rc) {
+    MbParams p = {};
+    p.X = reinterpret_cast<const f16*>(X);
+    p.M = (int32_t)M;
+    p.K = (int32_t)K;
+    p.ndesc = 1;
+    p.parts = parts;
+    p.d[0].W = W;
+    p.d[0].S = reinterpret_cast<const uint16_t*>(S);
+    p.d[0].Y = logits;
+    p.d[0].N = (int32_t)N;
+    MbPlan pl;
+    if (!plan_mb<MB_ARGMAX, float>(p, pl)) return 1;
+    *nparts = pl.nranges;
+    *rc = launch_mb<MB_ARGMAX, float>(p, pl, st);
+    return 0;
+}
+
+}  // namespace xhip_host
