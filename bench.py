@@ -125,7 +125,7 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--quick", action="store_true", help="headline config only")
-    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,cfg3,cfg4")
+    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
@@ -253,6 +253,24 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
     if want("cfg2"):
         for m in (1, 2, 4, 8):
             gemv_cfg(f"cfg2_down_m{m}_n5120_k17408", m, 5120, 17408)
+
+    if want("fused"):  # decode projections of forward_layer (forward.cpp:117-125, 237-247)
+        K = 5120
+        for name, Ns in (("qkv", (12288, 1024, 1024)), ("la_in_proj", (10240, 6144, 48, 48))):
+            rigs = [Rig(torch, dev, N, K, 0.02, seed=i) for i, N in enumerate(Ns)]
+            copies = min(r.copies for r in rigs)
+            X = torch.from_numpy(synth.activations(0, 1, K)).view(torch.float16).to(dev)
+            Ys = [torch.empty((1, N), dtype=torch.float16, device=dev) for N in Ns]
+            def fn(i, rigs=rigs, Ys=Ys, Ns=Ns, X=X):
+                ds = [ops.FusedProjectionDesc(Y, r.W[i], r.S[i], None, N) for Y, r, N in zip(Ys, rigs, Ns)]
+                ops.linear_int4_fused(X, ds, len(ds), 1, K)
+            w, e = time_launches(torch, fn, steps, warm, copies, graph=graph)
+            b = sum(gemv_bytes(1, N, K, N, 2) for N in Ns) - (len(Ns) - 1) * K * 2
+            record(f"fused_{name}_m1_k5120", {"M": 1, "N": list(Ns), "K": K, "us": round(e * 1e6, 3),
+                                             "GBps": round(b / e / 1e9, 1),
+                                             "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)})
+            del rigs
+        gemv_cfg("splitk_small_n48_m1_k5120", 1, 48, 5120)
 
     if want("cfg3"):   # LM head + argmax (ids only, logits not stored)
         N, K = 151936, 5120

@@ -66,6 +66,18 @@ inline void linear_int4(hipStream_t s, float* Y, const float* X, const uint8_t* 
                                                         M, N, K, group_size));
 }
 
+// src/targets/qwen3_8_27b/weights.h:13-23: what the runtime hands to the
+// projections (device pointers of a `.xinfer` weight and its scales).
+struct LinearWeightView {
+    void* d_weights_int4{nullptr};  // packed INT4 [out_features][in_features / 2]
+    void* d_scales{nullptr};        // fp16 [out_features][in_features / group_size]
+    int64_t in_features{0};
+    int64_t out_features{0};
+    int group_size{128};
+
+    bool is_valid() const noexcept { return d_weights_int4 != nullptr && d_scales != nullptr; }
+};
+
 // src/ops/linear.h:66-81
 struct FusedProjectionDesc {
     half* Y{nullptr};

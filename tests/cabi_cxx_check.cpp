@@ -25,6 +25,11 @@ int main() {
         if (e.status != XINFER_ERR_INVALID_ARG) ++failures;
     }
     if (argmax_scratch_size(4097, 1) != 16) ++failures;
+    LinearWeightView v;  // weights.h:13-23 defaults
+    if (v.is_valid() || v.group_size != 128) ++failures;
+    v.d_weights_int4 = (void*)0x1000;
+    v.d_scales = (void*)0x2000;
+    if (!v.is_valid()) ++failures;
     std::printf("%s\n", failures ? "FAIL" : "OK");
     return failures;
 }
