@@ -125,7 +125,7 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--quick", action="store_true", help="headline config only")
-    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,cfg3,cfg4")
+    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,crc,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
@@ -271,6 +271,26 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
                                              "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)})
             del rigs
         gemv_cfg("splitk_small_n48_m1_k5120", 1, 48, 5120)
+
+    if want("crc"):    # .xinfer section verification on the device (GPU CRC-64)
+        import ctypes
+        from xinfer_amd import _lib
+        L = _lib.load_library()
+        n = 256 << 20
+        bufs = [torch.randint(0, 256, (n,), dtype=torch.uint8, device=dev) for _ in range(3)]
+        crc_out = torch.zeros(1, dtype=torch.int64, device=dev)
+        scratch = torch.empty(L.xinfer_crc64_device_scratch_bytes(n), dtype=torch.uint8, device=dev)
+
+        def crc(i):
+            st = torch.cuda.current_stream().cuda_stream
+            _lib.check("xinfer_crc64_device", L.xinfer_crc64_device(
+                ctypes.c_void_p(st), ctypes.c_void_p(bufs[i].data_ptr()), n, ctypes.c_void_p(crc_out.data_ptr()),
+                ctypes.c_void_p(scratch.data_ptr()), scratch.numel()))
+        w, e = time_launches(torch, crc, 48, 6, len(bufs), graph=graph)
+        record("artifact_crc64_device_256MiB", {"bytes": n, "us": round(e * 1e6, 2),
+                                                "GBps": round(n / e / 1e9, 1),
+                                                "frac_hbm": round(n / e / 1e9 / HBM_PEAK_GBPS, 4)})
+        del bufs
 
     if want("cfg3"):   # LM head + argmax (ids only, logits not stored)
         N, K = 151936, 5120

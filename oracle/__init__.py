@@ -13,6 +13,7 @@ which restates the reference's CPU oracle loops:
 * ``argmax``       -- tests/test_ops_oracle.cpp:926-933, src/ops/sampling.cpp:75-85
 * ``dequant_int4`` -- tools/convert/qwen3_8_27b/convert.py:129-148
 * ``quantize_int4``-- tools/convert/qwen3_8_27b/convert.py:93-119
+* ``crc64``        -- src/artifact/checksum.cpp:10-54 (one byte per step)
 * ``f16``/``f32``  -- own IEEE binary16 conversion (round to nearest even)
 """
 from __future__ import annotations
@@ -63,6 +64,8 @@ def lib():
         L.oracle_argmax.argtypes = [_p, _i64]
         L.oracle_top2_margin.restype = ctypes.c_float
         L.oracle_top2_margin.argtypes = [_p, _i64]
+        L.oracle_crc64.restype = ctypes.c_uint64
+        L.oracle_crc64.argtypes = [_p, _i64]
         _lib = L
     return _lib
 
@@ -141,3 +144,21 @@ def argmax(logits) -> int:
 def top2_margin(logits) -> float:
     x = _c(logits, np.float32).reshape(-1)
     return float(lib().oracle_top2_margin(_ptr(x), x.size))
+
+
+def crc64(data) -> int:
+    """CRC-64/ECMA-182 (reflected) of bytes / a uint8 array."""
+    a = np.frombuffer(bytes(data), np.uint8) if isinstance(data, (bytes, bytearray, memoryview)) \
+        else _c(np.asarray(data).reshape(-1).view(np.uint8), np.uint8)
+    return int(lib().oracle_crc64(_ptr(a), a.size))
+
+
+# ------------------------------------------------------------------------
+# Reference artifact code built from /root/reference (oracle/_ref/artifact_ref):
+# the reference's own writer / reader / CRC, driven by ref_artifact_driver.cpp.
+_REF_TOOL = os.path.join(_HERE, "_ref", "artifact_ref")
+
+
+def ref_artifact_tool():
+    """Path of the reference-built artifact tool, or None when absent."""
+    return _REF_TOOL if os.path.exists(_REF_TOOL) else None

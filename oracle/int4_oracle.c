@@ -205,3 +205,24 @@ float oracle_top2_margin(const float* logits, int64_t V) {
         if (i != b && logits[i] > second) second = logits[i];
     return logits[b] - second;
 }
+
+/* --------------------------------------------------------------- CRC-64 ---- */
+
+/* src/artifact/checksum.cpp:10-54: table of the reflected polynomial, register
+ * starts at all ones, c = (c >> 8) ^ T[(c ^ byte) & 0xFF], result XOR all ones. */
+uint64_t oracle_crc64(const uint8_t* data, int64_t n) {
+    static uint64_t table[256];
+    static int ready = 0;
+    const uint64_t poly = 0xC96C5795D7870F42ULL;
+    if (!ready) {
+        for (uint64_t b = 0; b < 256; ++b) {
+            uint64_t c = b;
+            for (int i = 0; i < 8; ++i) c = (c & 1) ? (c >> 1) ^ poly : c >> 1;
+            table[b] = c;
+        }
+        ready = 1;
+    }
+    uint64_t c = 0xFFFFFFFFFFFFFFFFULL;
+    for (int64_t i = 0; i < n; ++i) c = (c >> 8) ^ table[(c ^ data[i]) & 0xFF];
+    return c ^ 0xFFFFFFFFFFFFFFFFULL;
+}

@@ -61,6 +61,10 @@ void oracle_swiglu_int4(float* Y, const float* X,
  * Returns 0 for V <= 1 (sampling.cpp:17-18). */
 int64_t oracle_argmax(const float* logits, int64_t V);
 
+/* CRC-64/ECMA-182, reflected, one byte per step: src/artifact/checksum.cpp:10-54
+ * (table generation :15-31, update :42-47, digest :49-51). */
+uint64_t oracle_crc64(const uint8_t* data, int64_t n);
+
 /* Second-largest value's gap: top1 - top2 (for reporting argmax margins). */
 float oracle_top2_margin(const float* logits, int64_t V);
 

@@ -1,6 +1,7 @@
 """CPU checks of the C-ABI library: it loads, exports every symbol the
 header declares, and rejects bad arguments before touching a device."""
 import ctypes
+import glob
 import os
 import re
 
@@ -9,13 +10,16 @@ import pytest
 from xinfer_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "xinfer_hip", "xinfer_ops.h")
+HEADERS = sorted(glob.glob(os.path.join(ROOT, "include", "xinfer_hip", "*.h")))
 
 
 def header_functions():
-    txt = open(HEADER).read()
-    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
-    return sorted(set(re.findall(r"\b(xinfer_\w+)\s*\(", txt)))
+    names = set()
+    for h in HEADERS:
+        txt = open(h).read()
+        txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+        names |= set(re.findall(r"\b(xinfer_\w+)\s*\(", txt))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")

@@ -1,4 +1,5 @@
-"""ctypes binding of libxinfer_hip.so (the C-ABI in include/xinfer_hip/xinfer_ops.h).
+"""ctypes binding of libxinfer_hip.so (the C-ABI in include/xinfer_hip/xinfer_ops.h and
+include/xinfer_hip/xinfer_artifact.h).
 
 Loading fails loudly when the library is missing: there is no CPU fallback.
 """
@@ -16,8 +17,10 @@ XINFER_ERR_UNSUPPORTED = -2
 XINFER_ERR_MISALIGNED = -3
 XINFER_ERR_HIP = -4
 XINFER_ERR_SCRATCH = -5
+XINFER_ERR_IO = -6
+XINFER_ERR_CHECKSUM = -7
 
-# Every symbol include/xinfer_hip/xinfer_ops.h declares.
+# Every symbol include/xinfer_hip/*.h declares.
 EXPORTS = (
     "xinfer_status_string",
     "xinfer_version",
@@ -34,6 +37,23 @@ EXPORTS = (
     "xinfer_lm_head_argmax_scratch_bytes",
     "xinfer_lm_head_argmax_int4",
     "xinfer_dequant_int4_f32",
+    # xinfer_artifact.h
+    "xinfer_crc64",
+    "xinfer_crc64_file",
+    "xinfer_crc64_device_scratch_bytes",
+    "xinfer_crc64_device",
+    "xinfer_artifact_open",
+    "xinfer_artifact_close",
+    "xinfer_artifact_header",
+    "xinfer_artifact_footer",
+    "xinfer_artifact_metadata_json",
+    "xinfer_artifact_section_count",
+    "xinfer_artifact_section_at",
+    "xinfer_artifact_section_by_name",
+    "xinfer_artifact_read_section",
+    "xinfer_artifact_validate_checksum",
+    "xinfer_artifact_upload_section",
+    "xinfer_artifact_load_linear",
 )
 
 
@@ -42,6 +62,31 @@ class XinferError(RuntimeError):
         self.status = status
         name = _lib.xinfer_status_string(status).decode() if _lib else str(status)
         super().__init__(f"{fn} failed: {name} ({status})")
+
+
+class FileHeader(ctypes.Structure):
+    """Mirror of ``xinfer_file_header`` (reference FileHeader, src/artifact/container.h:35-47)."""
+    _pack_ = 1
+    _fields_ = [("magic", ctypes.c_uint8 * 8), ("format_version", ctypes.c_uint32),
+                ("header_size", ctypes.c_uint32), ("flags", ctypes.c_uint32),
+                ("section_count", ctypes.c_uint32), ("metadata_offset", ctypes.c_uint64),
+                ("metadata_size", ctypes.c_uint64), ("section_table_offset", ctypes.c_uint64),
+                ("section_table_size", ctypes.c_uint64), ("total_file_size", ctypes.c_uint64)]
+
+
+class SectionInfo(ctypes.Structure):
+    """Mirror of ``xinfer_section_info`` (reference SectionEntry, src/artifact/container.h:50-58)."""
+    _pack_ = 1
+    _fields_ = [("name", ctypes.c_char * 96), ("type_tag", ctypes.c_uint32),
+                ("flags", ctypes.c_uint32), ("offset", ctypes.c_uint64),
+                ("size", ctypes.c_uint64), ("checksum", ctypes.c_uint64)]
+
+
+class LinearWeightViewC(ctypes.Structure):
+    """Mirror of ``xinfer_linear_weight_view`` (reference LinearWeightView, weights.h:13-23)."""
+    _fields_ = [("d_weights_int4", ctypes.c_void_p), ("d_scales", ctypes.c_void_p),
+                ("in_features", ctypes.c_int64), ("out_features", ctypes.c_int64),
+                ("group_size", ctypes.c_int32)]
 
 
 class FusedDesc(ctypes.Structure):
@@ -100,8 +145,47 @@ def load_library(path: str = None):
     L.xinfer_lm_head_argmax_int4.restype = ctypes.c_int
     L.xinfer_dequant_int4_f32.argtypes = [_p, _p, _p, _p, _i64, _i64, _i32]
     L.xinfer_dequant_int4_f32.restype = ctypes.c_int
+    _bind_artifact(L)
     _lib = L
     return L
+
+
+def _bind_artifact(L) -> None:
+    u64 = ctypes.c_uint64
+    cp = ctypes.c_char_p
+    L.xinfer_crc64.argtypes = [_p, _sz]
+    L.xinfer_crc64.restype = u64
+    L.xinfer_crc64_file.argtypes = [cp, u64]
+    L.xinfer_crc64_file.restype = u64
+    L.xinfer_crc64_device_scratch_bytes.argtypes = [_sz]
+    L.xinfer_crc64_device_scratch_bytes.restype = _sz
+    L.xinfer_crc64_device.argtypes = [_p, _p, _sz, _p, _p, _sz]
+    L.xinfer_crc64_device.restype = ctypes.c_int
+    L.xinfer_artifact_open.argtypes = [cp, ctypes.POINTER(_p), _p, _sz]
+    L.xinfer_artifact_open.restype = ctypes.c_int
+    L.xinfer_artifact_close.argtypes = [_p]
+    L.xinfer_artifact_close.restype = None
+    L.xinfer_artifact_header.argtypes = [_p, ctypes.POINTER(FileHeader)]
+    L.xinfer_artifact_header.restype = ctypes.c_int
+    L.xinfer_artifact_footer.argtypes = [_p, ctypes.POINTER(u64)]
+    L.xinfer_artifact_footer.restype = ctypes.c_int
+    L.xinfer_artifact_metadata_json.argtypes = [_p, ctypes.POINTER(_sz)]
+    L.xinfer_artifact_metadata_json.restype = _p
+    L.xinfer_artifact_section_count.argtypes = [_p]
+    L.xinfer_artifact_section_count.restype = _i32
+    L.xinfer_artifact_section_at.argtypes = [_p, _i32, ctypes.POINTER(SectionInfo)]
+    L.xinfer_artifact_section_at.restype = ctypes.c_int
+    L.xinfer_artifact_section_by_name.argtypes = [_p, cp, ctypes.POINTER(SectionInfo)]
+    L.xinfer_artifact_section_by_name.restype = ctypes.c_int
+    L.xinfer_artifact_read_section.argtypes = [_p, cp, _p, _sz, _p, _sz]
+    L.xinfer_artifact_read_section.restype = ctypes.c_int
+    L.xinfer_artifact_validate_checksum.argtypes = [_p, _p, _sz]
+    L.xinfer_artifact_validate_checksum.restype = ctypes.c_int
+    L.xinfer_artifact_upload_section.argtypes = [_p, cp, _p, _p, _sz, ctypes.c_int, _p, _sz]
+    L.xinfer_artifact_upload_section.restype = ctypes.c_int
+    L.xinfer_artifact_load_linear.argtypes = [_p, cp, _i64, _i64, _i32, _p,
+                                              ctypes.POINTER(LinearWeightViewC), _p, _sz]
+    L.xinfer_artifact_load_linear.restype = ctypes.c_int
 
 
 def check(fn: str, status: int) -> None:

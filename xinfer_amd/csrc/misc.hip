@@ -7,6 +7,7 @@
 // with a sign-extending bit-field extract, FP32 fma against FP32 X.
 
 #include "common.h"
+#include "../../include/xinfer_hip/xinfer_artifact.h"
 
 namespace xhip {
 
@@ -163,6 +164,8 @@ const char* xinfer_status_string(int status) {
         case XINFER_ERR_MISALIGNED: return "XINFER_ERR_MISALIGNED";
         case XINFER_ERR_HIP: return "XINFER_ERR_HIP";
         case XINFER_ERR_SCRATCH: return "XINFER_ERR_SCRATCH";
+        case XINFER_ERR_IO: return "XINFER_ERR_IO";
+        case XINFER_ERR_CHECKSUM: return "XINFER_ERR_CHECKSUM";
         default: return "XINFER_ERR_UNKNOWN";
     }
 }
