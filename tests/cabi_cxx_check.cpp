@@ -2,9 +2,10 @@
 // argument-validation paths, which return before any device work.
 #include <cstdio>
 
+#include "xinfer_hip/xinfer_artifact.hpp"
 #include "xinfer_hip/xinfer_ops.hpp"
 
-int main() {
+int main(int argc, char** argv) {
     using namespace xinfer::ops;
     int failures = 0;
     // empty shape: silent no-op, as src/ops/linear.cpp:176
@@ -30,6 +31,21 @@ int main() {
     v.d_weights_int4 = (void*)0x1000;
     v.d_scales = (void*)0x2000;
     if (!v.is_valid()) ++failures;
+    // artifact reader mirror (reader.h names) on a reference-written file
+    if (xinfer::artifact::Crc64::calculate("123456789", 9) != 0x995DC9BBDF1939FAULL) ++failures;
+    if (argc > 1) {
+        xinfer::artifact::ArtifactReader r;
+        std::string err;
+        if (!r.open(argv[1], &err) || !r.validate_checksum(&err)) ++failures;
+        const auto names = r.list_sections();
+        if (names.empty() || !r.has_section(names[0]) || r.has_section("no.such")) ++failures;
+        std::vector<uint8_t> data;
+        if (!r.read_section(names[0], data, &err) || data.size() != r.get_section_info(names[0])->size)
+            ++failures;
+        if (r.header().section_count != names.size()) ++failures;
+        xinfer::artifact::ArtifactReader bad;
+        if (bad.open("/nonexistent.xinfer", &err) || err.find("Could not open file") != 0) ++failures;
+    }
     std::printf("%s\n", failures ? "FAIL" : "OK");
     return failures;
 }

@@ -84,8 +84,9 @@ def test_scratch_sizes(L):
 
 
 def test_cxx_interface_compiles_links_and_validates(tmp_path):
-    """The C++ mirror of xinfer::ops builds with g++ against the C-ABI and its
-    validation paths behave (no GPU work is issued)."""
+    """The C++ mirrors (xinfer::ops, xinfer::artifact) build with g++ against
+    the C-ABI; validation paths and the host-side reader behave (no GPU work
+    is issued)."""
     import subprocess
     src = os.path.join(ROOT, "tests", "cabi_cxx_check.cpp")
     exe = str(tmp_path / "cabi_cxx_check")
@@ -95,5 +96,6 @@ def test_cxx_interface_compiles_links_and_validates(tmp_path):
                     "-L", libdir, "-lxinfer_hip", f"-Wl,-rpath,{libdir}", f"-Wl,-rpath,{torch_lib}",
                     f"-Wl,-rpath-link,{torch_lib}", "-L", torch_lib],
                    check=True)
-    r = subprocess.run([exe], capture_output=True, text=True, timeout=120)
+    golden = os.path.join(ROOT, "tests", "golden", "artifact_ref_small.xinfer")
+    r = subprocess.run([exe, golden], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and r.stdout.strip() == "OK", (r.stdout, r.stderr)
