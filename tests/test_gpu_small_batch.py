@@ -180,3 +180,22 @@ def test_small_batch_lm_head_ties_lowest_index():
     got = to_np(ids)
     for m in range(M):
         assert got[m] == oracle.argmax(ref[m])
+
+
+def test_lm_head_back_to_back_calls():
+    """Consecutive LM-head calls with new inputs (GEMV and small-batch kernels,
+    shared candidate scratch) each give the oracle's ids."""
+    import torch
+    ops = _ops()
+    N, K = 20000, 2048
+    W, S, _ = _inputs(77, 1, N, K, 0.01)
+    dW, dS = to_dev(W), f16_dev(S)
+    for M in (1, 4):
+        for call in range(4):
+            Xb = synth.activations(100 + 10 * M + call, M, K)
+            ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+            ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+            ops.lm_head_argmax_int4(ids, None, f16_dev(Xb), dW, dS, M, N, K)
+            got = to_np(ids)
+            for m in range(M):
+                assert got[m] == oracle.argmax(ref[m]), (M, call, m)
