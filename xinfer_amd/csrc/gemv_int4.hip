@@ -362,18 +362,27 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
                 if (arg_better(key, n, bv, bi)) { bv = key; bi = n; }
             }
         }
+        // thread t holds outputs with m == t % MR: reduce over lanes of the same
+        // m (lane exchanges at distances >= MR keep m), then over the waves
+#pragma unroll
+        for (int off = 32; off >= MR; off >>= 1) {
+            const float ov = __shfl_xor(bv, off);
+            const int32_t oi = __shfl_xor(bi, off);
+            if (arg_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+        }
         __syncthreads();  // partial slots are reused for the candidates below
         float* cv = part;
-        int32_t* ci = reinterpret_cast<int32_t*>(part + 256);
-        cv[tid] = bv;
-        ci[tid] = bi;
+        int32_t* ci = reinterpret_cast<int32_t*>(part + kWaves * MR);
+        if (lane < MR) {
+            cv[wave * MR + lane] = bv;
+            ci[wave * MR + lane] = bi;
+        }
         __syncthreads();
         if (tid < MR && tid < p.M) {
-            // thread t holds outputs with m == t % MR (256 is a multiple of MR)
-            float b = -__builtin_inff();
-            int32_t i = 0x7FFFFFFF;
-            for (int t = tid; t < 256; t += MR)
-                if (arg_better(cv[t], ci[t], b, i)) { b = cv[t]; i = ci[t]; }
+            float b = cv[tid];
+            int32_t i = ci[tid];
+            for (int w = 1; w < kWaves; ++w)
+                if (arg_better(cv[w * MR + tid], ci[w * MR + tid], b, i)) { b = cv[w * MR + tid]; i = ci[w * MR + tid]; }
             ArgCand o;
             o.v = b;
             o.i = i;
