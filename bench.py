@@ -125,7 +125,7 @@ def main():
     ap.add_argument("--steps", type=int, default=640)
     ap.add_argument("--warmup", type=int, default=64)
     ap.add_argument("--quick", action="store_true", help="headline config only")
-    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,crc,cfg3,cfg4")
+    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,norm,crc,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
@@ -271,6 +271,48 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
                                              "frac_hbm": round(b / e / 1e9 / HBM_PEAK_GBPS, 4)})
             del rigs
         gemv_cfg("splitk_small_n48_m1_k5120", 1, 48, 5120)
+
+    if want("norm"):   # RMSNorm prologue / residual epilogue, fused vs separate launches
+        K, Ns = 5120, (12288, 1024, 1024)
+        rigs = [Rig(torch, dev, N, K, 0.02, seed=i) for i, N in enumerate(Ns)]
+        copies = min(r.copies for r in rigs)
+        nw = torch.linspace(0.5, 1.5, K, dtype=torch.float32, device=dev)
+        for M in (1, 4):
+            X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+            Xn = torch.empty_like(X)
+            Ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
+
+            def fused(i, rigs=rigs, Ys=Ys, X=X, M=M):
+                ds = [ops.FusedProjectionDesc(Y, r.W[i], r.S[i], None, N) for Y, r, N in zip(Ys, rigs, Ns)]
+                ops.rmsnorm_linear_int4_fused(X, nw, 1e-6, ds, 3, M, K)
+
+            def separate(i, rigs=rigs, Ys=Ys, X=X, Xn=Xn, M=M):
+                ops.rmsnorm(Xn, X, nw, M, K, 1e-6)
+                ds = [ops.FusedProjectionDesc(Y, r.W[i], r.S[i], None, N) for Y, r, N in zip(Ys, rigs, Ns)]
+                ops.linear_int4_fused(Xn, ds, 3, M, K)
+            _, ef = time_launches(torch, fused, steps, warm, copies, graph=graph)
+            _, es = time_launches(torch, separate, steps, warm, copies, graph=graph)
+            record(f"rmsnorm_qkv_m{M}_k5120", {"M": M, "N": list(Ns), "K": K, "us_fused": round(ef * 1e6, 3),
+                                               "us_separate": round(es * 1e6, 3)})
+        del rigs
+        N, K = 5120, 6144                      # o_proj of a full-attention layer
+        rig = Rig(torch, dev, N, K, 0.02)
+        for M in (1, 4):
+            X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+            R = torch.zeros((M, N), dtype=torch.float16, device=dev)
+            Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+            def fused_r(i, X=X, R=R, M=M):
+                ops.linear_int4_residual(R, X, rig.W[i], rig.S[i], None, M, N, K)
+
+            def separate_r(i, X=X, R=R, Y=Y, M=M):
+                ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)
+                ops.add_inplace(R, Y, M * N)
+            _, ef = time_launches(torch, fused_r, steps, warm, rig.copies, graph=graph)
+            _, es = time_launches(torch, separate_r, steps, warm, rig.copies, graph=graph)
+            record(f"residual_oproj_m{M}_n5120_k6144", {"M": M, "N": N, "K": K, "us_fused": round(ef * 1e6, 3),
+                                                         "us_separate": round(es * 1e6, 3)})
+        del rig
 
     if want("crc"):    # .xinfer section verification on the device (GPU CRC-64)
         import ctypes

@@ -193,6 +193,51 @@ int xinfer_dequant_int4_f32(void* stream, float* out, const uint8_t* W_int4,
                             const void* scales, int64_t N, int64_t K,
                             int32_t group_size);
 
+/* ---------------------------------------------------------------------------
+ * The operations on either side of the projections in forward_layer
+ * (src/targets/qwen3_8/forward.cpp:112-125, 229, 270-290), standalone and
+ * fused into the projection kernels.
+ * ------------------------------------------------------------------------- */
+
+/* Replaces `rmsnorm(q, half* out, const half* in, const float* weight,
+ * num_tokens, hidden_size, eps)` -- src/ops/rmsnorm.h:17-23:
+ * out = fp16(in * (1 / sqrt(mean(in^2) + eps)) * weight), FP32 math. */
+int xinfer_rmsnorm_f16(void* stream, void* out, const void* in, const float* weight,
+                       int64_t num_tokens, int64_t hidden_size, float eps);
+
+/* Replaces `add_inplace(q, half* a, const half* b, n)` -- src/ops/elementwise.h:22:
+ * a = fp16(fp32(a) + fp32(b)). */
+int xinfer_add_inplace_f16(void* stream, void* a, const void* b, int64_t num_elements);
+
+/* rmsnorm (rmsnorm.h:17-23) fused with linear_int4_fused (linear.h:97-103):
+ * the input-norm + QKV / linear-attention in_proj pair of forward.cpp:112-125
+ * and :237-247.  The projections see exactly the fp16 normalised X that
+ * xinfer_rmsnorm_f16 would write (up to the order of the sum of squares).
+ * Decode shapes only: M <= 8 (XINFER_ERR_UNSUPPORTED otherwise; prefill
+ * callers run xinfer_rmsnorm_f16 first). */
+int xinfer_rmsnorm_linear_int4_fused_f16(void* stream, const void* X,
+                                         const float* norm_weight, float eps,
+                                         const xinfer_fused_desc* descs,
+                                         int32_t num_descs, int64_t M, int64_t K,
+                                         int32_t group_size);
+
+/* rmsnorm fused with mlp_gate_up_swiglu_int4 (linear.h:117-127): the
+ * post-attention norm + gate/up pair of forward.cpp:273-281.  M <= 8. */
+int xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
+                                               const float* norm_weight, float eps,
+                                               const uint8_t* W_gate, const void* scales_gate,
+                                               const uint8_t* W_up, const void* scales_up,
+                                               int64_t M, int64_t N, int64_t K,
+                                               int32_t group_size);
+
+/* linear_int4 (linear.h:30-39) fused with add_inplace (elementwise.h:22):
+ * residual[m][n] = fp16(residual + fp16(linear(X) + bias)), bit-identical to
+ * the pair at forward.cpp:229/270 and :284-290.  Any M. */
+int xinfer_linear_int4_residual_f16(void* stream, void* residual, const void* X,
+                                    const uint8_t* W_int4, const void* scales,
+                                    const float* bias, int64_t M, int64_t N,
+                                    int64_t K, int32_t group_size);
+
 #ifdef __cplusplus
 }
 #endif

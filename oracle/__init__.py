@@ -13,6 +13,8 @@ which restates the reference's CPU oracle loops:
 * ``argmax``       -- tests/test_ops_oracle.cpp:926-933, src/ops/sampling.cpp:75-85
 * ``dequant_int4`` -- tools/convert/qwen3_8_27b/convert.py:129-148
 * ``quantize_int4``-- tools/convert/qwen3_8_27b/convert.py:93-119
+* ``rmsnorm_f16``  -- src/ops/rmsnorm.cpp:45-78
+* ``add_inplace_f16`` -- src/ops/elementwise.cpp:213-231
 * ``crc64``        -- src/artifact/checksum.cpp:10-54 (one byte per step)
 * ``f16``/``f32``  -- own IEEE binary16 conversion (round to nearest even)
 """
@@ -64,6 +66,8 @@ def lib():
         L.oracle_argmax.argtypes = [_p, _i64]
         L.oracle_top2_margin.restype = ctypes.c_float
         L.oracle_top2_margin.argtypes = [_p, _i64]
+        L.oracle_rmsnorm_f16.argtypes = [_p, _p, _p, _i64, _i64, ctypes.c_float]
+        L.oracle_add_inplace_f16.argtypes = [_p, _p, _i64]
         L.oracle_crc64.restype = ctypes.c_uint64
         L.oracle_crc64.argtypes = [_p, _i64]
         _lib = L
@@ -144,6 +148,24 @@ def argmax(logits) -> int:
 def top2_margin(logits) -> float:
     x = _c(logits, np.float32).reshape(-1)
     return float(lib().oracle_top2_margin(_ptr(x), x.size))
+
+
+def rmsnorm_f16(x_bits, weight, eps=1e-6) -> np.ndarray:
+    """x_bits: uint16 [T, H] fp16 bit patterns -> uint16 [T, H]."""
+    x = _c(x_bits, np.uint16)
+    T, H = x.shape
+    w = _c(weight, np.float32)
+    out = np.zeros_like(x)
+    lib().oracle_rmsnorm_f16(_ptr(out), _ptr(x), _ptr(w), T, H, float(eps))
+    return out
+
+
+def add_inplace_f16(a_bits, b_bits) -> np.ndarray:
+    """Returns fp16(fp32(a) + fp32(b)) as uint16 (a copy; inputs untouched)."""
+    a = np.array(a_bits, np.uint16, copy=True)
+    b = _c(b_bits, np.uint16)
+    lib().oracle_add_inplace_f16(_ptr(a), _ptr(b), a.size)
+    return a
 
 
 def crc64(data) -> int:

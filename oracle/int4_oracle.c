@@ -226,3 +226,30 @@ uint64_t oracle_crc64(const uint8_t* data, int64_t n) {
     for (int64_t i = 0; i < n; ++i) c = (c >> 8) ^ table[(c ^ data[i]) & 0xFF];
     return c ^ 0xFFFFFFFFFFFFFFFFULL;
 }
+
+/* -------------------------------------------------- RMSNorm, add_inplace ---- */
+
+/* src/ops/rmsnorm.cpp:45-78. */
+void oracle_rmsnorm_f16(uint16_t* out, const uint16_t* in, const float* weight,
+                        int64_t tokens, int64_t hidden, float eps) {
+    for (int64_t t = 0; t < tokens; ++t) {
+        const uint16_t* x = in + t * hidden;
+        uint16_t* y = out + t * hidden;
+        float ss = 0.0f;
+        for (int64_t i = 0; i < hidden; ++i) {
+            const float v = oracle_half_to_float(x[i]);
+            ss += v * v;
+        }
+        const float inv = 1.0f / sqrtf(ss / (float)hidden + eps);
+        for (int64_t i = 0; i < hidden; ++i) {
+            const float v = oracle_half_to_float(x[i]);
+            y[i] = oracle_float_to_half(v * inv * weight[i]);
+        }
+    }
+}
+
+/* src/ops/elementwise.cpp:213-231. */
+void oracle_add_inplace_f16(uint16_t* a, const uint16_t* b, int64_t n) {
+    for (int64_t i = 0; i < n; ++i)
+        a[i] = oracle_float_to_half(oracle_half_to_float(a[i]) + oracle_half_to_float(b[i]));
+}

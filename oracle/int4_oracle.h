@@ -61,6 +61,14 @@ void oracle_swiglu_int4(float* Y, const float* X,
  * Returns 0 for V <= 1 (sampling.cpp:17-18). */
 int64_t oracle_argmax(const float* logits, int64_t V);
 
+/* RMSNorm, fp16 in/out, fp32 weight: src/ops/rmsnorm.cpp:45-78 (sum of squares
+ * in FP32 in index order, inv = 1 / sqrt(sum / H + eps), out = fp16(x * inv * w)). */
+void oracle_rmsnorm_f16(uint16_t* out, const uint16_t* in, const float* weight,
+                        int64_t tokens, int64_t hidden, float eps);
+
+/* add_inplace, fp16: src/ops/elementwise.cpp:213-231, a = fp16(fp32(a) + fp32(b)). */
+void oracle_add_inplace_f16(uint16_t* a, const uint16_t* b, int64_t n);
+
 /* CRC-64/ECMA-182, reflected, one byte per step: src/artifact/checksum.cpp:10-54
  * (table generation :15-31, update :42-47, digest :49-51). */
 uint64_t oracle_crc64(const uint8_t* data, int64_t n);

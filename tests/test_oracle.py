@@ -237,3 +237,59 @@ def test_golden_fixtures_reproduce():
             assert oracle.argmax(z["X"]) == int(z["Y"]), f
         elif kind == "dequant":
             assert np.array_equal(oracle.dequant_int4(z["W"], z["S"], N, K), z["Y"]), f
+
+
+# ------------------------------------------------------ RMSNorm, add ----
+
+def test_rmsnorm_matches_float64_formulation():
+    """The reference's own check (tests/test_ops_oracle.cpp:50-101): hidden 5120,
+    4 tokens, x ~ U(-1, 1), w ~ U(0, 2), sum of squares in double.  The fp16
+    oracle output must be that value rounded, give or take one fp16 ulp (the
+    FP32 sum's rounding can move a result across a rounding boundary)."""
+    rng = np.random.default_rng(42)
+    T, H, eps = 4, 5120, 1e-6
+    x = oracle.f32_to_f16(rng.uniform(-1, 1, (T, H)).astype(np.float32))
+    w = (rng.uniform(-1, 1, H) + 1.0).astype(np.float32)
+    got = oracle.f16_to_f32(oracle.rmsnorm_f16(x, w, eps)).astype(np.float64)
+    xf = oracle.f16_to_f32(x).astype(np.float64)
+    inv = 1.0 / np.sqrt((xf * xf).sum(1, keepdims=True) / H + eps)
+    ref = xf * inv * w
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    assert (np.abs(got - ref) <= ulp).all()
+    # a row scaled by 4 normalises to the same output (scale invariance,
+    # exact: powers of two commute with every rounding step)
+    got4 = oracle.rmsnorm_f16(oracle.f32_to_f16(oracle.f16_to_f32(x) * 4), w, 0.0)
+    assert np.array_equal(got4, oracle.rmsnorm_f16(x, w, 0.0))
+
+
+def test_rmsnorm_closed_forms():
+    H = 256
+    w = np.linspace(0.5, 1.5, H).astype(np.float32)
+    # constant row c: out = c / sqrt(c^2 + eps) * w
+    for c in (0.5, -2.0, 3.0):
+        x = oracle.f32_to_f16(np.full((1, H), c, np.float32))
+        got = oracle.f16_to_f32(oracle.rmsnorm_f16(x, w, 1e-6))[0]
+        assert np.allclose(got, np.sign(c) * w, rtol=1e-3)
+    # one-hot row e_j * a: out_j = sqrt(H) * w_j (eps = 0), zeros elsewhere
+    x = np.zeros((1, H), np.float32)
+    x[0, 17] = 2.0
+    got = oracle.f16_to_f32(oracle.rmsnorm_f16(oracle.f32_to_f16(x), w, 0.0))[0]
+    assert got[17] == oracle.f16_to_f32(oracle.f32_to_f16(np.array([16.0 * w[17]], np.float32)))[0]
+    assert (got[np.arange(H) != 17] == 0).all()
+    # zero row with eps > 0 stays zero, rows are independent
+    x = np.zeros((3, H), np.float32)
+    x[1] = 1.0
+    got = oracle.f16_to_f32(oracle.rmsnorm_f16(oracle.f32_to_f16(x), w, 1e-6))
+    assert (got[0] == 0).all() and (got[2] == 0).all() and np.allclose(got[1], w, rtol=1e-3)
+
+
+def test_add_inplace_matches_numpy_half():
+    rng = np.random.default_rng(5)
+    a = rng.integers(0, 65536, 200_000, dtype=np.uint32).astype(np.uint16)
+    b = rng.integers(0, 65536, 200_000, dtype=np.uint32).astype(np.uint16)
+    with np.errstate(all="ignore"):
+        ref = (a.view(np.float16).astype(np.float32) + b.view(np.float16).astype(np.float32)).astype(np.float16)
+    got = oracle.add_inplace_f16(a, b)
+    fin = np.isfinite(ref)
+    assert np.array_equal(got[fin], ref.view(np.uint16)[fin])
+    assert np.isnan(got.view(np.float16)[np.isnan(ref)]).all()

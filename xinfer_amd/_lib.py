@@ -37,6 +37,11 @@ EXPORTS = (
     "xinfer_lm_head_argmax_scratch_bytes",
     "xinfer_lm_head_argmax_int4",
     "xinfer_dequant_int4_f32",
+    "xinfer_rmsnorm_f16",
+    "xinfer_add_inplace_f16",
+    "xinfer_rmsnorm_linear_int4_fused_f16",
+    "xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16",
+    "xinfer_linear_int4_residual_f16",
     # xinfer_artifact.h
     "xinfer_crc64",
     "xinfer_crc64_file",
@@ -145,6 +150,19 @@ def load_library(path: str = None):
     L.xinfer_lm_head_argmax_int4.restype = ctypes.c_int
     L.xinfer_dequant_int4_f32.argtypes = [_p, _p, _p, _p, _i64, _i64, _i32]
     L.xinfer_dequant_int4_f32.restype = ctypes.c_int
+    f32 = ctypes.c_float
+    L.xinfer_rmsnorm_f16.argtypes = [_p, _p, _p, _p, _i64, _i64, f32]
+    L.xinfer_rmsnorm_f16.restype = ctypes.c_int
+    L.xinfer_add_inplace_f16.argtypes = [_p, _p, _p, _i64]
+    L.xinfer_add_inplace_f16.restype = ctypes.c_int
+    L.xinfer_rmsnorm_linear_int4_fused_f16.argtypes = [_p, _p, _p, f32, ctypes.POINTER(FusedDesc), _i32,
+                                                       _i64, _i64, _i32]
+    L.xinfer_rmsnorm_linear_int4_fused_f16.restype = ctypes.c_int
+    L.xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16.argtypes = [_p, _p, _p, _p, f32, _p, _p, _p, _p,
+                                                             _i64, _i64, _i64, _i32]
+    L.xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16.restype = ctypes.c_int
+    L.xinfer_linear_int4_residual_f16.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32]
+    L.xinfer_linear_int4_residual_f16.restype = ctypes.c_int
     _bind_artifact(L)
     _lib = L
     return L

@@ -91,6 +91,56 @@ __device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32
     return av > bv || (av == bv && ai < bi);
 }
 
+// ---- RMSNorm prologue (src/ops/rmsnorm.cpp:45-78) -----------------------
+// inv[m] = 1 / sqrt(mean_k(x[m][k]^2) + eps) for rows m < M of X (FP32 sums);
+// red: NTHREADS / 64 * 8 floats of LDS, inv: 8 floats of LDS.  Block-wide:
+// every thread must call it.
+template <int NTHREADS>
+__device__ inline void rms_inv_rows(const f16* X, int M, int K, float eps, float* red, float* inv) {
+    constexpr int NW = NTHREADS / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = K >> 3;  // 16-byte chunks per row
+    for (int m = 0; m < M; ++m) {
+        float ss = 0.0f;
+        for (int c = tid; c < c8; c += NTHREADS) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(X + (size_t)m * K + (size_t)c * 8);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f16x2 h = as_h2(w[j]);
+                const float a = (float)h.x, b = (float)h.y;
+                ss += a * a;
+                ss += b * b;
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+        if (lane == 0) red[m * NW + wave] = ss;
+    }
+    __syncthreads();
+    if (tid < M) {
+        float s = 0.0f;
+        for (int w = 0; w < NW; ++w) s += red[tid * NW + w];
+        inv[tid] = 1.0f / sqrtf(s / (float)K + eps);
+    }
+    __syncthreads();
+}
+
+// Normalise 8 consecutive activations (one 16-byte chunk starting at k):
+// x * inv * w[k] rounded to fp16, the expression of rmsnorm.cpp:78.
+__device__ inline u32x4 rms_apply8(u32x4 v, const float* w, float inv) {
+    uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f16x2 h = as_h2(a[j]);
+        f16x2 o;
+        o.x = (f16)((float)h.x * inv * w[2 * j]);
+        o.y = (f16)((float)h.y * inv * w[2 * j + 1]);
+        a[j] = as_u32(o);
+    }
+    return u32x4{a[0], a[1], a[2], a[3]};
+}
+
 }  // namespace xhip
 
 // Host-side helpers shared by the C-ABI translation units.

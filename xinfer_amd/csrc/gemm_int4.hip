@@ -44,6 +44,7 @@ struct GemmParams {
     int32_t M, N, K;
     int32_t mblocks, nranges;
     int32_t xcd_map;       // 1: XCD-aware block -> tile mapping
+    int32_t residual;      // plain fp16 Y: Y = fp16(Y + fp16(result))
 };
 
 constexpr int kGM = 128;      // block rows
@@ -299,7 +300,13 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
     // D layout of v_mfma_f32_16x16x32_f16: lane l holds rows 4*(l/16)+e,
     // e = 0..3, of column l%16.
     auto store = [&](int m, int n, float v) {
-        if (m < M && n < N) reinterpret_cast<OutT*>(p.Y)[(size_t)m * N + n] = (OutT)v;
+        if (m < M && n < N) {
+            OutT* y = reinterpret_cast<OutT*>(p.Y) + (size_t)m * N + n;
+            if (!SWIGLU && p.residual)  // add_inplace after the projection (elementwise.cpp:227)
+                *y = (OutT)((float)*y + (float)(OutT)v);
+            else
+                *y = (OutT)v;
+        }
     };
     auto bias_of = [&](int n) -> float { return (!SWIGLU && p.bias && n < N) ? p.bias[n] : 0.0f; };
 #pragma unroll
@@ -411,7 +418,7 @@ namespace xhip_host {
 // activation rows instead (correct, not tuned).
 int gemm_by_gemv_slabs(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
                        const uint16_t* S, const uint8_t* W2, const uint16_t* S2,
-                       const float* bias, int64_t M, int64_t N, int64_t K) {
+                       const float* bias, int64_t M, int64_t N, int64_t K, bool residual) {
     const size_t ysz = y_f32 ? 4 : 2;
     for (int64_t m0 = 0; m0 < M; m0 += 8) {
         const int64_t mm = (M - m0) < 8 ? (M - m0) : 8;
@@ -422,6 +429,8 @@ int gemm_by_gemv_slabs(hipStream_t st, void* Y, bool y_f32, const void* X, const
             rc = xinfer_mlp_gate_up_swiglu_int4_f16(st, Ys, Xs, W, S, W2, S2, mm, N, K, 128);
         else if (y_f32)
             rc = xinfer_linear_int4_f16_f32out(st, (float*)Ys, Xs, W, S, bias, mm, N, K, 128);
+        else if (residual)
+            rc = xinfer_linear_int4_residual_f16(st, Ys, Xs, W, S, bias, mm, N, K, 128);
         else
             rc = xinfer_linear_int4_f16(st, Ys, Xs, W, S, bias, mm, N, K, 128);
         if (rc) return rc;
@@ -431,8 +440,8 @@ int gemm_by_gemv_slabs(hipStream_t st, void* Y, bool y_f32, const void* X, const
 
 int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
                   const uint16_t* S, const uint8_t* W2, const uint16_t* S2, const float* bias,
-                  int64_t M, int64_t N, int64_t K) {
-    if (K % 1024 != 0) return gemm_by_gemv_slabs(st, Y, y_f32, X, W, S, W2, S2, bias, M, N, K);
+                  int64_t M, int64_t N, int64_t K, bool residual) {
+    if (K % 1024 != 0) return gemm_by_gemv_slabs(st, Y, y_f32, X, W, S, W2, S2, bias, M, N, K, residual);
     GemmParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.W = W;
@@ -444,6 +453,7 @@ int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint
     p.M = (int32_t)M;
     p.N = (int32_t)N;
     p.K = (int32_t)K;
+    p.residual = residual ? 1 : 0;
     if (W2) return launch_gemm<1, f16>(st, p);
     return y_f32 ? launch_gemm<0, float>(st, p) : launch_gemm<0, f16>(st, p);
 }

@@ -52,20 +52,25 @@ struct GemvDesc {
     int32_t N;
     int32_t rows_blk;    // rows per block (multiple of 2R)
     int32_t block_begin; // first block of this descriptor
-    int32_t pad;
+    int32_t residual;    // EPI_PLAIN, fp16 Y: Y = fp16(Y + fp16(result))
 };
 
 struct GemvParams {
     GemvDesc d[4];
     const f16* X;        // [M][K]
     ArgCand* parts;      // EPI_ARGMAX: [M][gridDim.x] block candidates
+    const float* norm_w; // RMSNorm weight [K] applied to X while staging (XLDS only), or null
+    float norm_eps;
     int32_t ndesc;
     int32_t M;           // real rows of X (<= MR)
     int32_t K;
-    int32_t pad;
 };
 
 constexpr int kWaves = 4;  // waves per 256-thread block
+// dynamic LDS in front of the X pieces: RMSNorm partial sums (kWaves * 8)
+// and the row factors (8), padded to keep the pieces 16-byte aligned
+constexpr int kGemvLdsHead = 256;
+static_assert((kWaves * 8 + 8) * 4 <= kGemvLdsHead, "RMSNorm scratch");
 
 template <int RR>
 struct ItemRegs {
@@ -135,9 +140,12 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
     // C [step][m][lane] (f32), padded to whole 1024-k steps; then partials.
     // A half-wave's piece read covers 512 contiguous bytes (no bank conflicts)
     // and the piece / m offsets are instruction immediates.
+    // The first kGemvLdsHead bytes hold the RMSNorm prologue's reduction.
     const int cpad = nsteps * 32;
-    u32x4* xs = reinterpret_cast<u32x4*>(smem);
-    float* xc = reinterpret_cast<float*>(smem + (size_t)(XLDS ? MR * 4 * cpad : 0) * 16);
+    float* rms_red = reinterpret_cast<float*>(smem);
+    float* rms_inv = rms_red + kWaves * 8;
+    u32x4* xs = reinterpret_cast<u32x4*>(smem + kGemvLdsHead);
+    float* xc = reinterpret_cast<float*>(smem + kGemvLdsHead + (size_t)(XLDS ? MR * 4 * cpad : 0) * 16);
     float* part = xc + (XLDS ? MR * cpad : 0);
     const int nslots = d.rows_blk * MR * E * nsteps;
 
@@ -204,6 +212,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
 
     // zero the partial slots; stage X (permuted) and the per-chunk bias terms
     for (int i = tid; i < nslots; i += 256) part[i] = 0.0f;
+    if (XLDS && p.norm_w) rms_inv_rows<256>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
     if (XLDS) {
         for (int i = tid; i < MR * cpad; i += 256) {
             const int m = i / cpad;
@@ -214,7 +223,10 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 u32x4 xv = u32x4{0u, 0u, 0u, 0u};  // padding chunks read as x = 0
-                if (c < cpr) xv = *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3));
+                if (c < cpr) {
+                    xv = *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3));
+                    if (p.norm_w) xv = rms_apply8(xv, p.norm_w + (c << 5) + (v << 3), rms_inv[mm]);
+                }
                 const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
                 f16x2 pr[4];
                 permute_x8(xa, pr);
@@ -402,7 +414,11 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
             } else if (d.bias) {
                 v += d.bias[n];
             }
-            reinterpret_cast<OutT*>(d.Y)[(size_t)m * N + n] = (OutT)v;
+            OutT* y = reinterpret_cast<OutT*>(d.Y) + (size_t)m * N + n;
+            if (EPI == EPI_PLAIN && d.residual)  // add_inplace after the projection (elementwise.cpp:227)
+                *y = (OutT)((float)*y + (float)(OutT)v);
+            else
+                *y = (OutT)v;
         }
     }
 }
@@ -591,7 +607,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
             rows = ((rows + 2 * r - 1) / (2 * r)) * (2 * r);
             size_t part = (size_t)rows * mr * E * nsteps * 4;
             if (EPI == EPI_ARGMAX && part < 2048) part = 2048;
-            lds = (xlds ? x_bytes : 0) + part;
+            lds = kGemvLdsHead + (xlds ? x_bytes : 0) + part;
             if (lds <= 64 * 1024) break;
             bpc *= 2;  // smaller row ranges until the partial slots fit
         }
@@ -600,7 +616,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
             const int64_t target = (int64_t)cus * occ;
             int64_t r2 = (total_rows + target - 1) / target;
             r2 = ((r2 + 2 * r - 1) / (2 * r)) * (2 * r);
-            if ((size_t)r2 * mr * E * nsteps * 4 + (xlds ? x_bytes : 0) <= 64 * 1024) rows = r2;
+            if (kGemvLdsHead + (size_t)r2 * mr * E * nsteps * 4 + (xlds ? x_bytes : 0) <= 64 * 1024) rows = r2;
         }
         best.mr = mr;
         best.r = r;
@@ -662,6 +678,7 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
     p.M = (int32_t)M;
     const GemvPlan pl = plan_gemv<EPI, OutT>(p, mr_for(M));
     if (pl.blocks <= 0) return XINFER_OK;
+    if (p.norm_w && !pl.xlds) return XINFER_ERR_UNSUPPORTED;  // the prologue runs while staging X
     launch_plan<EPI, OutT>(p, pl, st);
     return launch_status();
 }
@@ -673,22 +690,23 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
 // 1 when the shape is left to the VALU GEMV here).
 namespace xhip_host {
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-              int64_t M, int64_t K, int* rc);
+              int64_t M, int64_t K, const float* norm_w, float eps, bool residual, int* rc);
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
-              const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K, int* rc);
+              const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
+              const float* norm_w, float eps, int* rc);
 int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts);
 int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
               int64_t M, int64_t N, int64_t K, ArgCand* parts, int* nparts, int* rc);
 int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
                   const uint16_t* S, const uint8_t* W2, const uint16_t* S2, const float* bias,
-                  int64_t M, int64_t N, int64_t K);
+                  int64_t M, int64_t N, int64_t K, bool residual = false);
 }
 
 namespace {
 
 int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint8_t* W,
                     const void* S, const float* bias, int64_t M, int64_t N, int64_t K,
-                    int32_t G) {
+                    int32_t G, bool residual = false) {
     if (M <= 0 || N <= 0 || K <= 0) return XINFER_OK;
     int rc = check_common(M, N, K, G);
     if (rc) return rc;
@@ -699,11 +717,12 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
         return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (M > 8)
-        return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K);
+        return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K,
+                             residual);
     if (M >= 2) {
         const xinfer_fused_desc one = {Y, W, S, bias, N};
         int mrc = XINFER_OK;
-        if (!mb_linear(st, &one, 1, X, y_f32, M, K, &mrc)) return mrc;
+        if (!mb_linear(st, &one, 1, X, y_f32, M, K, nullptr, 0.0f, residual, &mrc)) return mrc;
     }
     GemvParams p = {};
     p.ndesc = 1;
@@ -714,36 +733,26 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     p.d[0].bias = bias;
     p.d[0].Y = Y;
     p.d[0].N = (int32_t)N;
+    p.d[0].residual = residual ? 1 : 0;
     return y_f32 ? gemv_f16<EPI_PLAIN, float>(st, p, M) : gemv_f16<EPI_PLAIN, f16>(st, p, M);
 }
 
-}  // namespace
-
-extern "C" {
-
-int xinfer_linear_int4_f16(void* stream, void* Y, const void* X, const uint8_t* W_int4,
-                           const void* scales, const float* bias, int64_t M, int64_t N,
-                           int64_t K, int32_t group_size) {
-    return linear_f16_impl(stream, Y, false, X, W_int4, scales, bias, M, N, K, group_size);
-}
-
-int xinfer_linear_int4_f16_f32out(void* stream, float* Y, const void* X, const uint8_t* W_int4,
-                                  const void* scales, const float* bias, int64_t M, int64_t N,
-                                  int64_t K, int32_t group_size) {
-    return linear_f16_impl(stream, Y, true, X, W_int4, scales, bias, M, N, K, group_size);
-}
-
-int xinfer_linear_int4_fused_f16(void* stream, const void* X, const xinfer_fused_desc* descs,
-                                 int32_t num_descs, int64_t M, int64_t K, int32_t group_size) {
+// linear_int4_fused with an optional RMSNorm prologue on X (norm_w != null:
+// decode shapes only, M <= 8, X staged in LDS).
+int fused_f16_impl(void* stream, const void* X, const xinfer_fused_desc* descs, int32_t num_descs,
+                   int64_t M, int64_t K, int32_t group_size, const float* norm_w, float eps) {
     if (!descs || num_descs <= 0 || num_descs > 4) return XINFER_ERR_INVALID_ARG;
     if (M <= 0 || K <= 0) return XINFER_OK;
     if (!X) return XINFER_ERR_INVALID_ARG;
     using namespace xhip_host;
-    if (!aligned(X, 16)) return XINFER_ERR_MISALIGNED;
+    if (!aligned(X, 16) || !aligned(norm_w, 4)) return XINFER_ERR_MISALIGNED;
+    if (norm_w && M > 8) return XINFER_ERR_UNSUPPORTED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     GemvParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     xinfer_fused_desc live[4];
     int nd = 0;
     for (int i = 0; i < num_descs; ++i) {
@@ -771,36 +780,39 @@ int xinfer_linear_int4_fused_f16(void* stream, const void* X, const xinfer_fused
     if (M > 8 || nd == 0) return XINFER_OK;
     if (M >= 2) {
         int mrc = XINFER_OK;
-        if (!mb_linear(st, live, nd, X, false, M, K, &mrc)) return mrc;
+        if (!mb_linear(st, live, nd, X, false, M, K, norm_w, eps, false, &mrc)) return mrc;
     }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);
 }
 
-int xinfer_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
-                                       const uint8_t* W_gate, const void* scales_gate,
-                                       const uint8_t* W_up, const void* scales_up, int64_t M,
-                                       int64_t N, int64_t K, int32_t group_size) {
+int swiglu_f16_impl(void* stream, void* Y, const void* X, const uint8_t* W_gate, const void* scales_gate,
+                    const uint8_t* W_up, const void* scales_up, int64_t M, int64_t N, int64_t K,
+                    int32_t group_size, const float* norm_w, float eps) {
     if (M <= 0 || N <= 0 || K <= 0) return XINFER_OK;
     int rc = check_common(M, N, K, group_size);
     if (rc) return rc;
     if (!Y || !X || !W_gate || !scales_gate || !W_up || !scales_up) return XINFER_ERR_INVALID_ARG;
     using namespace xhip_host;
     if (!aligned(W_gate, 16) || !aligned(W_up, 16) || !aligned(X, 16) || !aligned(Y, 2) ||
-        !aligned(scales_gate, 2) || !aligned(scales_up, 2))
+        !aligned(scales_gate, 2) || !aligned(scales_up, 2) || !aligned(norm_w, 4))
         return XINFER_ERR_MISALIGNED;
+    if (norm_w && M > 8) return XINFER_ERR_UNSUPPORTED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if (M > 8)
         return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
                              (const uint16_t*)scales_up, nullptr, M, N, K);
     if (M >= 2) {
         int mrc = XINFER_OK;
-        if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc)) return mrc;
+        if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, norm_w, eps, &mrc))
+            return mrc;
     }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     p.d[0].W = W_gate;
     p.d[0].S = reinterpret_cast<const uint16_t*>(scales_gate);
     p.d[0].W2 = W_up;
@@ -808,6 +820,58 @@ int xinfer_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
     p.d[0].Y = Y;
     p.d[0].N = (int32_t)N;
     return gemv_f16<EPI_SWIGLU, f16>(st, p, M);
+}
+
+}  // namespace
+
+extern "C" {
+
+int xinfer_linear_int4_f16(void* stream, void* Y, const void* X, const uint8_t* W_int4,
+                           const void* scales, const float* bias, int64_t M, int64_t N,
+                           int64_t K, int32_t group_size) {
+    return linear_f16_impl(stream, Y, false, X, W_int4, scales, bias, M, N, K, group_size);
+}
+
+int xinfer_linear_int4_f16_f32out(void* stream, float* Y, const void* X, const uint8_t* W_int4,
+                                  const void* scales, const float* bias, int64_t M, int64_t N,
+                                  int64_t K, int32_t group_size) {
+    return linear_f16_impl(stream, Y, true, X, W_int4, scales, bias, M, N, K, group_size);
+}
+
+int xinfer_linear_int4_fused_f16(void* stream, const void* X, const xinfer_fused_desc* descs,
+                                 int32_t num_descs, int64_t M, int64_t K, int32_t group_size) {
+    return fused_f16_impl(stream, X, descs, num_descs, M, K, group_size, nullptr, 0.0f);
+}
+
+int xinfer_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
+                                       const uint8_t* W_gate, const void* scales_gate,
+                                       const uint8_t* W_up, const void* scales_up, int64_t M,
+                                       int64_t N, int64_t K, int32_t group_size) {
+    return swiglu_f16_impl(stream, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, group_size,
+                           nullptr, 0.0f);
+}
+
+int xinfer_rmsnorm_linear_int4_fused_f16(void* stream, const void* X, const float* norm_weight,
+                                         float eps, const xinfer_fused_desc* descs, int32_t num_descs,
+                                         int64_t M, int64_t K, int32_t group_size) {
+    if (!norm_weight) return XINFER_ERR_INVALID_ARG;
+    return fused_f16_impl(stream, X, descs, num_descs, M, K, group_size, norm_weight, eps);
+}
+
+int xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
+                                               const float* norm_weight, float eps,
+                                               const uint8_t* W_gate, const void* scales_gate,
+                                               const uint8_t* W_up, const void* scales_up, int64_t M,
+                                               int64_t N, int64_t K, int32_t group_size) {
+    if (!norm_weight) return XINFER_ERR_INVALID_ARG;
+    return swiglu_f16_impl(stream, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, group_size,
+                           norm_weight, eps);
+}
+
+int xinfer_linear_int4_residual_f16(void* stream, void* residual, const void* X, const uint8_t* W_int4,
+                                    const void* scales, const float* bias, int64_t M, int64_t N,
+                                    int64_t K, int32_t group_size) {
+    return linear_f16_impl(stream, residual, false, X, W_int4, scales, bias, M, N, K, group_size, true);
 }
 
 size_t xinfer_lm_head_argmax_scratch_bytes(int64_t M, int64_t N, int64_t K) {

@@ -54,7 +54,7 @@ struct MbDesc {
     int32_t N;
     int32_t block_begin; // first block of this descriptor
     int32_t range_begin; // first tile range of this descriptor (counters, parts)
-    int32_t pad;
+    int32_t residual;    // MB_PLAIN, fp16 Y: Y = fp16(Y + fp16(result))
 };
 
 struct MbParams {
@@ -72,7 +72,8 @@ struct MbParams {
     int32_t gps;         // groups per k-slice (the last slice may be shorter)
     int32_t tiles_blk;   // 16-row tiles per block
     int32_t nranges;     // tile ranges over all descriptors
-    int32_t pad;
+    float norm_eps;
+    const float* norm_w; // RMSNorm weight [K] applied to X while staging, or null
 };
 
 constexpr uint32_t kOutOfRange = 0xFFFFF000u;  // >= every buffer resource size used here
@@ -142,14 +143,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 
     // LDS: X slice as MFMA A operands [group][dword t][k-quarter][m] (16 B
     // each), then the block's results [row][m][e] (fp32), then the argmax
-    // candidates of the waves (NW values, NW indices) and one flag word.
+    // candidates of the waves (NW values, NW indices), one flag word (padded
+    // to 16 bytes) and the RMSNorm prologue's sums and row factors.
     f16x8* xs = reinterpret_cast<f16x8*>(smem);
     float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * M * 16);
     float* candv = outl + (size_t)p.tiles_blk * 16 * M * E;
     int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
     int32_t* flag = candi + NW;
+    float* rms_red = reinterpret_cast<float*>(flag + 4);  // RMSNorm sums [NW * 8], factors [8]
+    float* rms_inv = rms_red + NW * 8;
 
-    // stage X[:, slice] (permuted to the decode's pair order)
+    // stage X[:, slice] (permuted to the decode's pair order); with an RMSNorm
+    // prologue the rows' scale factors come from the whole of K first
+    if (p.norm_w) rms_inv_rows<NT>(p.X, M, K, p.norm_eps, rms_red, rms_inv);
     {
         const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
         for (int i = tid; i < chunks; i += NT) {
@@ -160,6 +166,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             u32x4 xv[4];
 #pragma unroll
             for (int v = 0; v < 4; ++v) xv[v] = src[v];
+            if (p.norm_w) {
+                const float* wk = p.norm_w + (size_t)(g0 + gl) * 128 + cq * 32;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) xv[v] = rms_apply8(xv[v], wk + 8 * v, rms_inv[m]);
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const uint32_t xa[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
@@ -381,7 +392,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             } else if (d.bias) {
                 v += d.bias[n];
             }
-            reinterpret_cast<OutT*>(d.Y)[(size_t)m * N + n] = (OutT)v;
+            OutT* y = reinterpret_cast<OutT*>(d.Y) + (size_t)m * N + n;
+            if (EPI == MB_PLAIN && d.residual)  // add_inplace after the projection (elementwise.cpp:227)
+                *y = (OutT)((float)*y + (float)(OutT)v);
+            else
+                *y = (OutT)v;
         }
     }
 }
@@ -517,7 +532,8 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     // a partial last chunk of T > 1 costs decode and MFMA work)
     int t = ov.t > 0 ? ov.t : 1;
     t = t >= 2 ? 2 : 1;
-    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 + 2 * nw * 4 + 16;
+    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 + 2 * nw * 4 + 16 +
+                       (size_t)(nw * 8 + 8) * 4;
     if (lds > kMaxLds) return false;
     if (ks > 1 && ranges > (int64_t)kMaxRanges) return false;
     for (int i = 0; ks > 1 && i < p.ndesc; ++i)  // 32-bit buffer offsets into the partials
@@ -584,13 +600,16 @@ int launch_mb(const MbParams& p0, const MbPlan& pl, hipStream_t st) {
 // Entry points used by the GEMV front end (gemv_int4.hip).  Return 1 when the
 // shape is not handled here (the caller then runs the VALU GEMV).
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-              int64_t M, int64_t K, int* rc) {
+              int64_t M, int64_t K, const float* norm_w, float eps, bool residual, int* rc) {
     MbParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.M = (int32_t)M;
     p.K = (int32_t)K;
     p.ndesc = nd;
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     for (int i = 0; i < nd; ++i) {
+        p.d[i].residual = residual ? 1 : 0;
         p.d[i].W = descs[i].W_int4;
         p.d[i].S = reinterpret_cast<const uint16_t*>(descs[i].scales);
         p.d[i].bias = descs[i].bias;
@@ -605,8 +624,11 @@ int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void
 }
 
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
-              const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K, int* rc) {
+              const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
+              const float* norm_w, float eps, int* rc) {
     MbParams p = {};
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     p.X = reinterpret_cast<const f16*>(X);
     p.M = (int32_t)M;
     p.K = (int32_t)K;

@@ -6,6 +6,8 @@
 // arithmetic over speed: one 32-lane team per output row, nibbles decoded
 // with a sign-extending bit-field extract, FP32 fma against FP32 X.
 
+#include <algorithm>
+
 #include "common.h"
 #include "../../include/xinfer_hip/xinfer_artifact.h"
 
@@ -125,6 +127,32 @@ __global__ void dequant_int4_kernel(float* out, const uint8_t* W, const uint16_t
     }
 }
 
+// RMSNorm of one token per block (src/ops/rmsnorm.cpp:45-78): FP32 sum of
+// squares, inv = 1 / sqrt(mean + eps), out = fp16(x * inv * w).
+__global__ __launch_bounds__(256) void rmsnorm_f16_kernel(f16* out, const f16* in, const float* w,
+                                                          int32_t H, float eps) {
+    __shared__ float red[4];
+    const f16* x = in + (size_t)blockIdx.x * H;
+    f16* y = out + (size_t)blockIdx.x * H;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const float v = (float)x[i];
+        ss += v * v;
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
+    for (int i = threadIdx.x; i < H; i += 256) y[i] = (f16)((float)x[i] * inv * w[i]);
+}
+
+// a = fp16(fp32(a) + fp32(b)) (src/ops/elementwise.cpp:213-231)
+__global__ __launch_bounds__(256) void add_inplace_f16_kernel(f16* a, const f16* b, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        a[i] = (f16)((float)a[i] + (float)b[i]);
+}
+
 }  // namespace xhip
 
 using namespace xhip;
@@ -171,6 +199,27 @@ const char* xinfer_status_string(int status) {
 }
 
 const char* xinfer_version(void) { return "xinfer_hip 0.1.0 gfx950"; }
+
+int xinfer_rmsnorm_f16(void* stream, void* out, const void* in, const float* weight,
+                       int64_t num_tokens, int64_t hidden_size, float eps) {
+    if (num_tokens <= 0 || hidden_size <= 0) return XINFER_OK;
+    if (!out || !in || !weight) return XINFER_ERR_INVALID_ARG;
+    if (num_tokens > (1LL << 30) || hidden_size > (1LL << 30)) return XINFER_ERR_UNSUPPORTED;
+    hipLaunchKernelGGL(rmsnorm_f16_kernel, dim3((unsigned)num_tokens), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<f16*>(out),
+                       reinterpret_cast<const f16*>(in), weight, (int32_t)hidden_size, eps);
+    return xhip_host::launch_status();
+}
+
+int xinfer_add_inplace_f16(void* stream, void* a, const void* b, int64_t num_elements) {
+    if (num_elements <= 0) return XINFER_OK;
+    if (!a || !b) return XINFER_ERR_INVALID_ARG;
+    const int64_t blocks = std::min<int64_t>((num_elements + 255) / 256, 65536);
+    hipLaunchKernelGGL(add_inplace_f16_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<f16*>(a),
+                       reinterpret_cast<const f16*>(b), num_elements);
+    return xhip_host::launch_status();
+}
 
 int xinfer_linear_int4_f32(void* stream, float* Y, const float* X, const uint8_t* W_int4,
                            const void* scales, const float* bias, int64_t M, int64_t N, int64_t K,

@@ -125,3 +125,50 @@ def dequant_int4(out: torch.Tensor, W_int4, scales, N, K, group_size=128, stream
     L = load_library()
     check("dequant_int4", L.xinfer_dequant_int4_f32(_stream(stream), _ptr(out), _ptr(W_int4),
                                                     _ptr(scales), N, K, group_size))
+
+
+# ---- operations on either side of the projections (forward.cpp:112-125, 229, 270-290)
+
+def rmsnorm(out: torch.Tensor, inp: torch.Tensor, weight: torch.Tensor, num_tokens: int,
+            hidden_size: int, eps: float = 1e-6, stream=None) -> None:
+    """src/ops/rmsnorm.h:17-23 (fp16 in/out, fp32 weight)."""
+    L = load_library()
+    check("rmsnorm", L.xinfer_rmsnorm_f16(_stream(stream), _ptr(out), _ptr(inp), _ptr(weight),
+                                          num_tokens, hidden_size, float(eps)))
+
+
+def add_inplace(a: torch.Tensor, b: torch.Tensor, num_elements: int, stream=None) -> None:
+    """src/ops/elementwise.h:22 (fp16): a = fp16(fp32(a) + fp32(b))."""
+    L = load_library()
+    check("add_inplace", L.xinfer_add_inplace_f16(_stream(stream), _ptr(a), _ptr(b), num_elements))
+
+
+def rmsnorm_linear_int4_fused(X: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                              descs: Sequence[FusedProjectionDesc], num_descs: int, M: int, K: int,
+                              group_size: int = 128, stream=None) -> None:
+    """rmsnorm(X) then linear_int4_fused, in one launch (decode: M <= 8)."""
+    L = load_library()
+    arr = (FusedDesc * max(1, num_descs))()
+    for i in range(min(num_descs, len(descs))):
+        d = descs[i]
+        arr[i] = FusedDesc(_ptr(d.Y), _ptr(d.W_int4), _ptr(d.scales), _ptr(d.bias), d.N)
+    check("rmsnorm_linear_int4_fused", L.xinfer_rmsnorm_linear_int4_fused_f16(
+        _stream(stream), _ptr(X), _ptr(norm_weight), float(eps), arr, num_descs, M, K, group_size))
+
+
+def rmsnorm_mlp_gate_up_swiglu_int4(Y, X, norm_weight, eps, W_gate, scales_gate, W_up, scales_up,
+                                    M, N, K, group_size=128, stream=None) -> None:
+    """rmsnorm(X) then mlp_gate_up_swiglu_int4, in one launch (decode: M <= 8)."""
+    L = load_library()
+    check("rmsnorm_mlp_gate_up_swiglu_int4", L.xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(
+        _stream(stream), _ptr(Y), _ptr(X), _ptr(norm_weight), float(eps), _ptr(W_gate), _ptr(scales_gate),
+        _ptr(W_up), _ptr(scales_up), M, N, K, group_size))
+
+
+def linear_int4_residual(residual: torch.Tensor, X, W_int4, scales, bias, M, N, K, group_size=128,
+                         stream=None) -> None:
+    """residual += linear_int4(X) with the rounding of linear_int4 + add_inplace."""
+    L = load_library()
+    check("linear_int4_residual", L.xinfer_linear_int4_residual_f16(
+        _stream(stream), _ptr(residual), _ptr(X), _ptr(W_int4), _ptr(scales), _ptr(bias), M, N, K,
+        group_size))
