@@ -72,6 +72,7 @@ struct MbParams {
     int32_t gps;         // groups per k-slice (the last slice may be shorter)
     int32_t tiles_blk;   // 16-row tiles per block
     int32_t nranges;     // tile ranges over all descriptors
+    int32_t lkw;         // log2 of the waves that share a run of tiles, splitting its groups
     float norm_eps;
     const float* norm_w; // RMSNorm weight [K] applied to X while staging, or null
 };
@@ -82,6 +83,9 @@ constexpr uint32_t kOutOfRange = 0xFFFFF000u;  // >= every buffer resource size 
 // 128-byte line of its row.  Weights are loaded with the default cache policy
 // (measured faster here than the streaming hint: the other half of each line
 // is read by the same wave a few instructions later).
+#ifndef XHIP_MB_PF
+#define XHIP_MB_PF 3
+#endif
 #ifndef XHIP_MB_GP
 #define XHIP_MB_GP 2
 #endif
@@ -93,10 +97,10 @@ constexpr int kGP = XHIP_MB_GP;  // 128-k groups per item
 // loads do not hit stale lines of another XCD's L2.
 constexpr int kDeviceCoherent = 16;
 
-template <int TT>
+template <int E>
 struct MbItem {
-    u32x4 w[TT * kGP];
-    uint32_t s[TT * kGP];  // raw fp16 scale bits, converted at use
+    u32x4 w[E * kGP];
+    uint32_t s[E * kGP];  // raw fp16 scale bits, converted at use
 };
 
 __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
@@ -106,10 +110,9 @@ __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
     return r;
 }
 
-template <int T, int EPI, typename OutT, int NW, int PF>
+template <int MR, int EPI, typename OutT, int NW>
 __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p) {
-    constexpr int E = (EPI == MB_SWIGLU) ? 2 : 1;  // sums per output
-    constexpr int TT = T * E;                      // weight tiles per item
+    constexpr int E = (EPI == MB_SWIGLU) ? 2 : 1;  // sums per output (weight tiles per item)
     constexpr int NT = 64 * NW;
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -141,57 +144,36 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     const int ngs = min(p.gps, ng - g0);
     const uint32_t row_bytes = (uint32_t)K >> 1;
 
-    // LDS: X slice as MFMA A operands [group][dword t][k-quarter][m] (16 B
-    // each), then the block's results [row][m][e] (fp32), then the argmax
+    // LDS: X slice as MFMA A operands [group][dword t][k-quarter][m < MR] (16 B
+    // each), then the block's results [wave of the run][row][m][e] (fp32:
+    // one slice per wave sharing a run, summed in order), then the argmax
     // candidates of the waves (NW values, NW indices), one flag word (padded
     // to 16 bytes) and the RMSNorm prologue's sums and row factors.
     f16x8* xs = reinterpret_cast<f16x8*>(smem);
-    float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * M * 16);
-    float* candv = outl + (size_t)p.tiles_blk * 16 * M * E;
+    float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * MR * 16);
+    float* candv = outl + ((size_t)p.tiles_blk * 16 * M * E << p.lkw);
     int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
     int32_t* flag = candi + NW;
     float* rms_red = reinterpret_cast<float*>(flag + 4);  // RMSNorm sums [NW * 8], factors [8]
     float* rms_inv = rms_red + NW * 8;
 
-    // stage X[:, slice] (permuted to the decode's pair order); with an RMSNorm
-    // prologue the rows' scale factors come from the whole of K first
-    if (p.norm_w) rms_inv_rows<NT>(p.X, M, K, p.norm_eps, rms_red, rms_inv);
-    {
-        const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
-        for (int i = tid; i < chunks; i += NT) {
-            const int m = i % M;
-            const int q = i / M;
-            const int cq = q & 3, gl = q >> 2;
-            const u32x4* src = reinterpret_cast<const u32x4*>(p.X + (size_t)m * K + (size_t)(g0 + gl) * 128 + cq * 32);
-            u32x4 xv[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v) xv[v] = src[v];
-            if (p.norm_w) {
-                const float* wk = p.norm_w + (size_t)(g0 + gl) * 128 + cq * 32;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) xv[v] = rms_apply8(xv[v], wk + 8 * v, rms_inv[m]);
-            }
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const uint32_t xa[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
-                f16x2 pr[4];
-                permute_x8(xa, pr);
-                xs[((gl * 4 + t) * 4 + cq) * M + m] = pack_q8(pr);
-            }
-        }
-    }
+    // Waves come in runs of kw = 2^lkw: the waves of a run share its tiles
+    // and split the slice's groups evenly (every wave gets at least one
+    // group: the host keeps kw <= groups per slice).  A wave walks its
+    // tiles one at a time, all of its groups per tile.
+    const int lkw = p.lkw;
+    const int kp = wave & ((1 << lkw) - 1);  // this wave's part of the groups
+    const int nr = NW >> lkw;                // runs per block
+    const int wr = wave >> lkw;
+    const int t0 = (wr * tiles_here) / nr;
+    const int t1 = ((wr + 1) * tiles_here) / nr;
+    const int gb = (kp * ngs) >> lkw;                   // first group of this wave
+    const int ngw = (((kp + 1) * ngs) >> lkw) - gb;     // groups of this wave (>= 1)
+    const int nig = (ngw + kGP - 1) / kGP;  // items per tile
+    const int nreal = (t1 - t0) * nig;
 
-    // this wave's run of tiles, processed T at a time (the last chunk may be
-    // partial: its missing tiles load nothing and are never stored)
-    const int t0 = (wave * tiles_here) / NW;
-    const int t1 = ((wave + 1) * tiles_here) / NW;
-    const int nchunks = (t1 - t0 + T - 1) / T;
-    const int nig = (ngs + kGP - 1) / kGP;  // items per chunk
-    const int nreal = nchunks * nig;
-
-    const uint32_t srow_bytes = (uint32_t)ng * 2u;
     const int nrec_w = (int)((uint32_t)N * row_bytes);
-    const int nrec_s = (int)((uint32_t)N * srow_bytes);
+    const int nrec_s = (int)((uint32_t)N * (uint32_t)ng * 2u);
     const __amdgpu_buffer_rsrc_t rw0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.W, (short)0, nrec_w, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.S, (short)0, nrec_s, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -199,102 +181,161 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
         (void*)(EPI == MB_SWIGLU ? d.S2 : d.S), (short)0, nrec_s, 0x00020000);
 
-    // load cursor: (chunk, group in slice) of the next item; wave-uniform
-    int lc = 0, lgl = 0, lcount = nreal;
-    auto load_next = [&](MbItem<TT>& b) {
-        const bool item_ok = lcount > 0;
-        --lcount;
+    // Every load is in bounds, so the addressing needs no per-lane checks:
+    // a lane's row offset is set once per tile (rows past N read row N - 1
+    // and are never stored), the group offset is wave-uniform (the buffer
+    // instruction's scalar offset), and a padding group past the wave's
+    // last reloads that last group and gets a zero scale in the compute.
+    uint32_t vw = 0, vs = 0;  // lane offsets (bytes) of the load tile's row at the wave's first group
+    auto set_tile = [&](int tile) {
+        const uint32_t n = (uint32_t)min(n0 + tile * 16 + l16, N - 1);
+        vw = n * row_bytes + (uint32_t)(g0 + gb) * 64u + (uint32_t)kq * 16u;
+        vs = (n * (uint32_t)ng + (uint32_t)(g0 + gb)) * 2u;
+    };
+    set_tile(t0);
+    int lt = t0, lg = 0, lrem = nreal;  // load cursor (wave-uniform): tile, item, items left
+    auto load_next = [&](MbItem<E>& b) {
 #pragma unroll
-        for (int j = 0; j < T; ++j) {
-            const int tile = t0 + lc * T + j;
-            const int n = n0 + tile * 16 + l16;
-            const bool ok = item_ok && tile < t1 && n < N;
+        for (int gi = 0; gi < kGP; ++gi) {
+            const int g = min(lg * kGP + gi, ngw - 1);
 #pragma unroll
-            for (int gi = 0; gi < kGP; ++gi) {
-                const int gl = lgl * kGP + gi;
-                const bool okg = ok && (kGP == 1 || gl < ngs);
-                const uint32_t wo = okg ? (uint32_t)n * row_bytes + (uint32_t)(g0 + gl) * 64u + (uint32_t)kq * 16u
-                                        : kOutOfRange;
-                const uint32_t so = okg ? ((uint32_t)n * (uint32_t)ng + (uint32_t)(g0 + gl)) * 2u : kOutOfRange;
-#pragma unroll
-                for (int e = 0; e < E; ++e) {
-                    b.w[(j * E + e) * kGP + gi] =
-                        __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)wo, 0, XHIP_MB_AUX);
-                    b.s[(j * E + e) * kGP + gi] = __builtin_amdgcn_raw_buffer_load_b16(e ? rs1 : rs0, (int)so, 0, 0);
-                }
+            for (int e = 0; e < E; ++e) {
+                b.w[e * kGP + gi] =
+                    __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)vw, g * 64, XHIP_MB_AUX);
+                b.s[e * kGP + gi] = __builtin_amdgcn_raw_buffer_load_b16(e ? rs1 : rs0, (int)vs, g * 2, 0);
             }
         }
-        if (++lgl == nig) { lgl = 0; ++lc; }
+        // past the last item the cursor stays: the extra loads repeat it
+        if (--lrem > 0 && ++lg == nig) {
+            lg = 0;
+            set_tile(++lt);
+        }
     };
 
-    MbItem<TT> buf[PF + 1];
+    constexpr int PF = XHIP_MB_PF;  // items in flight per wave
+    MbItem<E> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
 
+    // Stage X[:, slice] (permuted to the decode's pair order) while the
+    // first weight items are in flight.  Each thread issues the loads of up
+    // to kStageUnroll chunks before it waits for any, so the staging costs
+    // one memory latency instead of one per chunk round.  With an RMSNorm
+    // prologue the rows' scale factors come from the whole of K first.
+    if (p.norm_w) rms_inv_rows<NT>(p.X, M, K, p.norm_eps, rms_red, rms_inv);
+    {
+        constexpr int kStageUnroll = 4;
+        const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
+        for (int i0 = tid; i0 < chunks; i0 += NT * kStageUnroll) {
+            u32x4 xv[kStageUnroll][4];
+#pragma unroll
+            for (int u = 0; u < kStageUnroll; ++u) {
+                const int i = i0 + u * NT;
+                if (i < chunks) {
+                    const int m = i % M;
+                    const int q = i / M;
+                    const u32x4* src = reinterpret_cast<const u32x4*>(
+                        p.X + (size_t)m * K + (size_t)(g0 + (q >> 2)) * 128 + (q & 3) * 32);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) xv[u][v] = src[v];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kStageUnroll; ++u) {
+                const int i = i0 + u * NT;
+                if (i < chunks) {
+                    const int m = i % M;
+                    const int q = i / M;
+                    const int cq = q & 3, gl = q >> 2;
+                    if (p.norm_w) {
+                        const float* wk = p.norm_w + (size_t)(g0 + gl) * 128 + cq * 32;
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) xv[u][v] = rms_apply8(xv[u][v], wk + 8 * v, rms_inv[m]);
+                    }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t xa[4] = {xv[u][t].x, xv[u][t].y, xv[u][t].z, xv[u][t].w};
+                        f16x2 pr[4];
+                        permute_x8(xa, pr);
+                        xs[((gl * 4 + t) * 4 + cq) * MR + m] = pack_q8(pr);
+                    }
+                }
+            }
+        }
+    }
     __syncthreads();  // X staged
 
-    f32x4 acc[TT];
+    f32x4 acc[E];
 #pragma unroll
-    for (int j = 0; j < TT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int x = 0; x < E; ++x) acc[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int mm = l16 < M ? l16 : M - 1;
-    auto compute_item = [&](int it, const MbItem<TT>& b) {
+    // A operands: lane l reads row m = l % 16 (rows past M repeat row M - 1;
+    // their results are never stored) of k-quarter l / 16; the stride of m
+    // is the compile-time MR, so the four dwords of a group are immediate
+    // offsets from one address.
+    const f16x8* xl = xs + kq * MR + (l16 < M ? l16 : M - 1);
+    auto compute_item = [&](int it, const MbItem<E>& b) {
+        f16x8 xa[kGP][4];
+        int gl[kGP];
 #pragma unroll
         for (int gi = 0; gi < kGP; ++gi) {
-            const int gl = min(it * kGP + gi, ngs - 1);  // a padding group has w = 0
-            f16x8 xa[4];
+            gl[gi] = it * kGP + gi;
+            const f16x8* xg = xl + (gb + min(gl[gi], ngw - 1)) * (16 * MR);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xa[t] = xs[((gl * 4 + t) * 4 + kq) * M + mm];
+            for (int t = 0; t < 4; ++t) xa[gi][t] = xg[t * 4 * MR];
+        }
 #pragma unroll
-            for (int j = 0; j < TT; ++j) {
-                const u32x4 wv = b.w[j * kGP + gi];
-                const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
-                f32x4 c = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int x = 0; x < E; ++x) {
+            // the groups' MFMA chains are independent: interleaved
+            f32x4 c[kGP];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
+            for (int gi = 0; gi < kGP; ++gi) c[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+#pragma unroll
+                for (int gi = 0; gi < kGP; ++gi) {
+                    const u32x4 wv = b.w[x * kGP + gi];
+                    const uint32_t wd = t == 0 ? wv.x : t == 1 ? wv.y : t == 2 ? wv.z : wv.w;
                     f16x2 q[4];
-                    dequant8(wd[t], q);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[t], pack_q8(q), c, 0, 0, 0);
+                    dequant8(wd, q);
+                    c[gi] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa[gi][t], pack_q8(q), c[gi], 0, 0, 0);
                 }
-                const float s = h2f((uint16_t)b.s[j * kGP + gi]);
+            }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) acc[j][e] = __builtin_fmaf(s, c[e], acc[j][e]);
+            for (int gi = 0; gi < kGP; ++gi) {
+                const float s = gl[gi] < ngw ? h2f((uint16_t)b.s[x * kGP + gi]) : 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[x][e] = __builtin_fmaf(s, c[gi][e], acc[x][e]);
             }
         }
     };
 
     // D layout of the 16x16 MFMA: lane l holds rows m = 4 * (l / 16) + e
     // (e = 0..3) of column n = l % 16.
-    auto flush = [&](int c) {
+    auto flush = [&](int tile) {
 #pragma unroll
-        for (int j = 0; j < T; ++j) {
-            const int tile = t0 + c * T + j;
-            if (tile < t1) {
+        for (int e = 0; e < 4; ++e) {
+            const int m = 4 * kq + e;
+            if (m < M) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int m = 4 * kq + e;
-                    if (m < M) {
-#pragma unroll
-                        for (int x = 0; x < E; ++x)
-                            outl[((tile * 16 + l16) * M + m) * E + x] = acc[j * E + x][e];
-                    }
-                }
+                for (int x = 0; x < E; ++x)
+                    outl[((((kp * p.tiles_blk) + tile) * 16 + l16) * M + m) * E + x] = acc[x][e];
             }
         }
 #pragma unroll
-        for (int j = 0; j < TT; ++j) acc[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int x = 0; x < E; ++x) acc[x] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     };
 
-    int cc = 0, cgl = 0;
+    int ct = t0, cgl = 0;  // compute cursor: tile, item
     for (int base = 0; base < nreal; base += PF + 1) {
 #pragma unroll
         for (int j = 0; j <= PF; ++j) {
             load_next(buf[(j + PF) % (PF + 1)]);
-            compute_item(min(cgl, nig - 1), buf[j]);
+            compute_item(cgl, buf[j]);
             if (base + j < nreal && ++cgl == nig) {
-                flush(cc);
+                flush(ct);
                 cgl = 0;
-                ++cc;
+                ++ct;
             }
         }
     }
@@ -302,6 +343,15 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 
     // ---- epilogue over the block's rows x M (n fastest: coalesced stores)
     const int nout = rows_here * M;
+    if (lkw > 0) {  // sum the run's slices in slice order
+        const int sl = p.tiles_blk * 16 * M * E;
+        for (int o = tid; o < nout * E; o += NT) {
+            float v = outl[o];
+            for (int q = 1; q < (1 << lkw); ++q) v += outl[q * sl + o];
+            outl[o] = v;
+        }
+        __syncthreads();
+    }
     if (ks > 1) {
         // partials [slice][e][m][n] of this descriptor (< 2 GiB: checked on the host)
         const uint32_t sst = (uint32_t)p.ws_slice[di];
@@ -316,10 +366,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
                     (int)(((uint32_t)slice * sst + ((uint32_t)x * M + m) * (uint32_t)N + n0 + rl) * 4u), 0,
                     kDeviceCoherent);
         }
-        // Device-coherent stores and loads keep the partials consistent across
-        // the XCDs' L2s without a device-wide fence (which would write back and
-        // invalidate every L2 once per block).  The barrier waits for this
-        // block's stores to complete before the arrival is counted.
+        // The partials are written and read only with device-coherent (sc1)
+        // accesses, the form of agent-scope atomic stores and loads, so they
+        // are consistent across the XCDs' L2s without a release write-back or
+        // an acquire invalidate of the L2.  Each wave waits for its stores to
+        // be acknowledged before the barrier, and the arrival is counted
+        // after the barrier; the last arriver's loads are issued after it has
+        // seen the count (control dependency through the flag).
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
         if (tid == 0) {
             const uint32_t old = __hip_atomic_fetch_add(&p.cnt[grange], 1u, __ATOMIC_RELAXED,
@@ -328,17 +382,24 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
         }
         __syncthreads();
         if (flag[0] == 0) return;  // another slice of this range finishes it
-        // acquire: drop lines of this XCD's L2 that may hold stale partials
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         for (int o = tid; o < nout; o += NT) {
             const int m = o / rows_here, rl = o - m * rows_here;
 #pragma unroll
             for (int x = 0; x < E; ++x) {
+                // slices in order, the loads of 8 slices in flight at a time
+                const uint32_t off = (((uint32_t)x * M + m) * (uint32_t)N + n0 + rl) * 4u;
                 float v = 0.0f;
-                for (int s = 0; s < ks; ++s)
-                    v += __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                        rws, (int)(((uint32_t)s * sst + ((uint32_t)x * M + m) * (uint32_t)N + n0 + rl) * 4u), 0,
-                        kDeviceCoherent));
+                for (int s0 = 0; s0 < ks; s0 += 8) {
+                    float pv[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        pv[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                            rws, (int)(s0 + u < ks ? (uint32_t)(s0 + u) * sst * 4u + off : kOutOfRange), 0,
+                            kDeviceCoherent));
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+                        if (s0 + u < ks) v += pv[u];
+                }
                 outl[(rl * M + m) * E + x] = v;
             }
         }
@@ -411,16 +472,16 @@ namespace {
 
 typedef void (*MbKernel)(MbParams);
 
-template <int T, int EPI, typename OutT>
+template <int MR, int EPI, typename OutT>
 MbKernel mb_pick_nw(int nw) {
-    return nw >= 16 ? gemv_mb_int4_kernel<T, EPI, OutT, 16, 3>
-         : nw >= 8  ? gemv_mb_int4_kernel<T, EPI, OutT, 8, 3>
-                    : gemv_mb_int4_kernel<T, EPI, OutT, 4, 3>;
+    return nw >= 16 ? gemv_mb_int4_kernel<MR, EPI, OutT, 16>
+         : nw >= 8  ? gemv_mb_int4_kernel<MR, EPI, OutT, 8>
+                    : gemv_mb_int4_kernel<MR, EPI, OutT, 4>;
 }
 
 template <int EPI, typename OutT>
-MbKernel mb_kernel_for(int t, int nw) {
-    return t >= 2 ? mb_pick_nw<2, EPI, OutT>(nw) : mb_pick_nw<1, EPI, OutT>(nw);
+MbKernel mb_kernel_for(int mr, int nw) {
+    return mr <= 4 ? mb_pick_nw<4, EPI, OutT>(nw) : mb_pick_nw<8, EPI, OutT>(nw);
 }
 
 int env_int(const char* name, int dflt) {
@@ -429,12 +490,13 @@ int env_int(const char* name, int dflt) {
 }
 
 struct MbOverrides {
-    int t, nw, ks, bpc, min_m;
+    int nw, ks, bpc, min_m, raise, kw;
 };
 const MbOverrides& mb_overrides() {
-    static const MbOverrides o = {env_int("XINFER_MB_T", 0), env_int("XINFER_MB_NW", 0),
+    static const MbOverrides o = {env_int("XINFER_MB_NW", 0),
                                   env_int("XINFER_MB_KS", 0), env_int("XINFER_MB_BPC", 0),
-                                  env_int("XINFER_MB_MIN_M", 0)};
+                                  env_int("XINFER_MB_MIN_M", 0), env_int("XINFER_MB_RAISE", -1),
+                                  env_int("XINFER_MB_KW", 0)};
     return o;
 }
 
@@ -476,7 +538,7 @@ bool mb_workspace(size_t ws_bytes, float** ws, uint32_t** cnt) {
 namespace xhip_host {
 
 struct MbPlan {
-    int t, nw, ks, gps, tiles_blk, blocks, nranges;
+    int mr, nw, ks, gps, tiles_blk, blocks, nranges, kw;
     size_t lds, ws_floats;
     MbKernel k;
 };
@@ -486,9 +548,15 @@ struct MbPlan {
 //   ks:  the smallest number of k-slices whose X slice fits the LDS budget,
 //        raised while the tile ranges alone cannot give every CU `bpc`
 //        blocks (short N, long K); argmax keeps ks = 1.
-//   tiles per block: the tiles spread evenly over cus * bpc / ks ranges,
-//        at least one per wave.
-//   T:   tiles per wave item (1 unless overridden).
+//   tiles per block: the tiles spread evenly over cus * bpc / ks ranges.
+//   kw:  waves per run of tiles, splitting the slice's groups (every wave
+//        has a tile of its run): the smallest power of two that gives at
+//        least half as many blocks as CUs, at most the waves of a block and
+//        the groups of the shortest slice.  This adds blocks to short-N
+//        shapes without a cross-block combine; more waves per tile than
+//        that measured slower (each wave then decodes fewer groups per
+//        fixed prologue).
+//   MR:  the m stride of the staged X (4 for M <= 4, else 8).
 template <int EPI, typename OutT>
 bool plan_mb(MbParams& p, MbPlan& pl) {
     const MbOverrides& ov = mb_overrides();
@@ -500,7 +568,8 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     const int cus = num_cus();
     int64_t tiles_total = 0;
     for (int i = 0; i < p.ndesc; ++i) tiles_total += (p.d[i].N + 15) / 16;
-    const size_t xg = (size_t)M * 256;  // LDS bytes of X per group
+    const int mr = M <= 4 ? 4 : 8;
+    const size_t xg = (size_t)mr * 256;  // LDS bytes of X per group
     const size_t x_budget = EPI == MB_ARGMAX ? 96 * 1024 : 48 * 1024;
     int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
     if (EPI == MB_ARGMAX) ks = 1;
@@ -514,10 +583,9 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
         int64_t rt = target / ks;
         if (rt < 1) rt = 1;
         tiles_blk = (tiles_total + rt - 1) / rt;
-        if (tiles_blk < nw) tiles_blk = nw;
         ranges = 0;
         for (int i = 0; i < p.ndesc; ++i) ranges += ((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk;
-        if (pass == 0 && ov.ks <= 0 && EPI != MB_ARGMAX && ranges * ks < target) {
+        if (pass == 0 && ov.ks <= 0 && ov.raise != 0 && EPI != MB_ARGMAX && ranges * ks < target) {
             int ks2 = (int)(target / ranges);
             if (ks2 > ng) ks2 = ng;
             if (ks2 > ks) { ks = ks2; continue; }
@@ -526,26 +594,35 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     }
     const int gps = (ng + ks - 1) / ks;
     ks = (ng + gps - 1) / gps;
-    const int per_wave = (int)((tiles_blk + nw - 1) / nw);
-    (void)per_wave;
-    // T = 1 measured fastest on every MI355X shape tried (waves own 1-5 tiles;
-    // a partial last chunk of T > 1 costs decode and MFMA work)
-    int t = ov.t > 0 ? ov.t : 1;
-    t = t >= 2 ? 2 : 1;
-    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 + 2 * nw * 4 + 16 +
+    const int last = ng - (ks - 1) * gps;  // groups of the shortest slice
+    int kw_cap = 1;
+    while (kw_cap * 2 <= nw && kw_cap * 2 <= last) kw_cap *= 2;
+    const int64_t tiles_want = tiles_blk;
+    int kw = 1;
+    for (;; kw *= 2) {
+        if (ov.kw > 0 && kw * 2 <= ov.kw && kw < kw_cap) continue;
+        tiles_blk = tiles_want < nw / kw ? nw / kw : tiles_want;  // every run of waves has a tile
+        ranges = 0;
+        for (int i = 0; i < p.ndesc; ++i) ranges += ((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk;
+        if (ov.kw > 0 || kw >= kw_cap || ranges * ks * 2 >= cus) break;
+    }
+    int lkw = 0;
+    while ((1 << lkw) < kw) ++lkw;
+    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16 +
                        (size_t)(nw * 8 + 8) * 4;
     if (lds > kMaxLds) return false;
     if (ks > 1 && ranges > (int64_t)kMaxRanges) return false;
     for (int i = 0; ks > 1 && i < p.ndesc; ++i)  // 32-bit buffer offsets into the partials
         if ((int64_t)ks * (E * M * p.d[i].N + 64) * 4 >= (1LL << 31)) return false;
-    pl.t = t;
+    pl.mr = mr;
     pl.nw = nw;
     pl.ks = ks;
     pl.gps = gps;
     pl.tiles_blk = (int)tiles_blk;
     pl.nranges = (int)ranges;
+    pl.kw = kw;
     pl.lds = lds;
-    pl.k = mb_kernel_for<EPI, OutT>(t, nw);
+    pl.k = mb_kernel_for<EPI, OutT>(mr, nw);
     int blocks = 0, rbeg = 0;
     int64_t wsoff = 0;
     for (int i = 0; i < p.ndesc; ++i) {
@@ -570,6 +647,7 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     p.gps = gps;
     p.tiles_blk = (int)tiles_blk;
     p.nranges = (int)ranges;
+    p.lkw = lkw;
     return true;
 }
 
