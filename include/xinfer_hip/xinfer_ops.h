@@ -213,8 +213,10 @@ int xinfer_add_inplace_f16(void* stream, void* a, const void* b, int64_t num_ele
  * the input-norm + QKV / linear-attention in_proj pair of forward.cpp:112-125
  * and :237-247.  The projections see exactly the fp16 normalised X that
  * xinfer_rmsnorm_f16 would write (up to the order of the sum of squares).
- * Decode shapes only: M <= 8 (XINFER_ERR_UNSUPPORTED otherwise; prefill
- * callers run xinfer_rmsnorm_f16 first). */
+ * Any M: at M = 1 the norm runs inside the projection kernel; otherwise the
+ * normalised rows go through a per-device library buffer (allocated on the
+ * first call of a size, so capture a graph after a warm-up call; calls on
+ * different streams of one device must not overlap). */
 int xinfer_rmsnorm_linear_int4_fused_f16(void* stream, const void* X,
                                          const float* norm_weight, float eps,
                                          const xinfer_fused_desc* descs,
@@ -222,7 +224,8 @@ int xinfer_rmsnorm_linear_int4_fused_f16(void* stream, const void* X,
                                          int32_t group_size);
 
 /* rmsnorm fused with mlp_gate_up_swiglu_int4 (linear.h:117-127): the
- * post-attention norm + gate/up pair of forward.cpp:273-281.  M <= 8. */
+ * post-attention norm + gate/up pair of forward.cpp:273-281.  Any M, as
+ * xinfer_rmsnorm_linear_int4_fused_f16. */
 int xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
                                                const float* norm_weight, float eps,
                                                const uint8_t* W_gate, const void* scales_gate,

@@ -57,7 +57,7 @@ def _xin(seed, M, K, scale=1.0):
     return oracle.f32_to_f16(rng.uniform(-scale, scale, (M, K)).astype(np.float32))
 
 
-@pytest.mark.parametrize("T,H", [(4, 5120), (1, 128), (7, 17408), (3, 1000), (300, 5120)])
+@pytest.mark.parametrize("T,H", [(4, 5120), (1, 128), (7, 17408), (3, 1000), (300, 5120), (2, 1001), (5, 24)])
 def test_rmsnorm_vs_oracle(T, H):
     import torch
     ops = _ops()
@@ -112,7 +112,8 @@ def test_rmsnorm_fused_qkv_descs(M):
     assert np.array_equal(_bits(dX), x)          # the input itself is not normalised in place
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (3, 640, 17408)])
+@pytest.mark.parametrize("M,N,K", [(1, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (3, 640, 17408),
+                                   (1, 640, 17408), (2, 640, 17408), (2, 4096, 5120)])
 def test_rmsnorm_fused_swiglu(M, N, K):
     import torch
     from scipy.special import expit
@@ -130,18 +131,31 @@ def test_rmsnorm_fused_swiglu(M, N, K):
     assert expit is not None
 
 
-def test_rmsnorm_fused_rejects_prefill_rows():
-    """The prologue is a decode fusion (the whole X row is read by every
-    block); prefill keeps the standalone rmsnorm, so M > 8 is refused."""
+@pytest.mark.parametrize("M", [9, 64])
+def test_rmsnorm_fused_prefill_rows(M):
+    """Beyond decode sizes the norm runs as its own kernel into a library
+    buffer that the projection (GEMM path) reads; same results."""
     import torch
     ops = _ops()
-    M, N, K = 9, 64, 256
-    Y = _empty((M, N), torch.float16)
-    W, S = synth.packed_weights(1, N, K), synth.scales(1, N, K)
-    with pytest.raises(RuntimeError):
-        ops.rmsnorm_linear_int4_fused(f16_dev(_xin(1, M, K)), to_dev(_norm_w(1, K)), 1e-6,
-                                      [ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, N)],
-                                      1, M, K)
+    K, Ns = 1024, (256, 128)
+    x, w = _xin(200 + M, M, K, 2.0), _norm_w(3, K, 0.5, 1.5)
+    descs, refs, outs = [], [], []
+    for p, N in enumerate(Ns):
+        W, S = synth.packed_weights(80 + p, N, K), synth.scales(80 + p, N, K)
+        refs.append(_ref_linear_after_norm(x, w, W, S, M, N, K))
+        Y = _empty((M, N), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, N))
+    ops.rmsnorm_linear_int4_fused(f16_dev(x), to_dev(w), 1e-6, descs, 2, M, K)
+    for Y, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Y), ref))
+    Wg, Wu = synth.packed_weights(8, 256, K), synth.packed_weights(8, 256, K, synth.STREAM_W2)
+    Sg, Su = synth.scales(8, 256, K), synth.scales(8, 256, K, stream=synth.STREAM_S2)
+    Y = _empty((M, 256), torch.float16)
+    ops.rmsnorm_mlp_gate_up_swiglu_int4(Y, f16_dev(x), to_dev(w), 1e-6, to_dev(Wg), f16_dev(Sg),
+                                        to_dev(Wu), f16_dev(Su), M, 256, K)
+    xn = oracle.f16_to_f32(oracle.rmsnorm_f16(x, w, 1e-6))
+    print(check_f16_tol(to_np(Y), oracle.swiglu_int4(xn, Wg, Sg, Wu, Su, M, 256, K)))
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 5120, 6144), (1, 5120, 17408), (4, 5120, 17408),

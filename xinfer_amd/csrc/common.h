@@ -90,38 +90,94 @@ __device__ __forceinline__ float argmax_key(float v, int64_t idx) {
 __device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32_t bi) {
     return av > bv || (av == bv && ai < bi);
 }
-
-// ---- RMSNorm prologue (src/ops/rmsnorm.cpp:45-78) -----------------------
-// inv[m] = 1 / sqrt(mean_k(x[m][k]^2) + eps) for rows m < M of X (FP32 sums);
-// red: NTHREADS / 64 * 8 floats of LDS, inv: 8 floats of LDS.  Block-wide:
-// every thread must call it.
+// Per-row RMSNorm factors of X [M][K] (M <= 8, K a multiple of 8) for a
+// block of NTHREADS threads: inv[m] = 1 / sqrt(sum_k x^2 / K + eps), the FP32
+// sum of src/ops/rmsnorm.cpp:45-71 (summed in a fixed order here, so every
+// block and every call get the same bits).  A power-of-two group of threads
+// owns each row and keeps up to 8 of its 16-byte loads in flight.
+// red: NTHREADS / 32 floats of LDS; inv: M floats of LDS.
 template <int NTHREADS>
 __device__ inline void rms_inv_rows(const f16* X, int M, int K, float eps, float* red, float* inv) {
-    constexpr int NW = NTHREADS / 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x;
+    const int mp = M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8;  // rows rounded up to a power of two
+    const int tpr = NTHREADS / mp;                             // threads per row (>= 32)
+    const int seg = tpr < 64 ? tpr : 64;                       // lanes reduced by shuffles
+    const int m = tid / tpr, r = tid - m * tpr;
     const int c8 = K >> 3;  // 16-byte chunks per row
-    for (int m = 0; m < M; ++m) {
-        float ss = 0.0f;
-        for (int c = tid; c < c8; c += NTHREADS) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(X + (size_t)m * K + (size_t)c * 8);
-            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+    float ss = 0.0f;
+    if (m < M) {
+        const u32x4* row = reinterpret_cast<const u32x4*>(X + (size_t)m * K);
+        for (int c0 = r; c0 < c8; c0 += tpr * 8) {
+            u32x4 v[8];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f16x2 h = as_h2(w[j]);
-                const float a = (float)h.x, b = (float)h.y;
-                ss += a * a;
-                ss += b * b;
+            for (int u = 0; u < 8; ++u) {
+                const int c = c0 + u * tpr;
+                v[u] = c < c8 ? row[c] : u32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const f16x2 h = as_h2(w[j]);
+                    const float a = (float)h.x, b = (float)h.y;
+                    ss += a * a;
+                    ss += b * b;
+                }
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-        if (lane == 0) red[m * NW + wave] = ss;
     }
+    for (int off = seg >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((tid & (seg - 1)) == 0) red[tid / seg] = ss;
     __syncthreads();
     if (tid < M) {
+        const int nseg = tpr / seg;
         float s = 0.0f;
-        for (int w = 0; w < NW; ++w) s += red[tid * NW + w];
+        for (int j = 0; j < nseg; ++j) s += red[tid * nseg + j];
         inv[tid] = 1.0f / sqrtf(s / (float)K + eps);
+    }
+    __syncthreads();
+}
+
+// Sum of squares of the 32 fp16 values of four 16-byte chunks, in order.
+__device__ inline float sumsq32(const u32x4* v) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t w[4] = {v[c].x, v[c].y, v[c].z, v[c].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f16x2 h = as_h2(w[j]);
+            const float a = (float)h.x, b = (float)h.y;
+            ss += a * a;
+            ss += b * b;
+        }
+    }
+    return ss;
+}
+
+// Finish of the one-pass RMSNorm prologue (the block stages all of K and
+// sums the squares of what it loaded): ssm[m] is this thread's partial sum
+// of row m (zero for rows it did not load).  Rows are reduced per wave by
+// shuffles, then over the waves in order, so the bits are the same on every
+// call.  red: NTHREADS / 64 * 8 floats of LDS; inv: M floats of LDS.
+template <int NTHREADS>
+__device__ inline void rms_finish_rows(const float (&ssm)[8], int M, int K, float eps, float* red, float* inv) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        if (m < M) {
+            float v = ssm[m];
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (lane == 0) red[wave * 8 + m] = v;
+        }
+    }
+    __syncthreads();
+    if ((int)threadIdx.x < M) {
+        float s = 0.0f;
+        for (int w = 0; w < NTHREADS / 64; ++w) s += red[w * 8 + threadIdx.x];
+        inv[threadIdx.x] = 1.0f / sqrtf(s / (float)K + eps);
     }
     __syncthreads();
 }

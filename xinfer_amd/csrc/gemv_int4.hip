@@ -212,9 +212,21 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
 
     // zero the partial slots; stage X (permuted) and the per-chunk bias terms
     for (int i = tid; i < nslots; i += 256) part[i] = 0.0f;
-    if (XLDS && p.norm_w) rms_inv_rows<256>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
+    // RMSNorm prologue: when X is staged in at most two rounds the row sums
+    // come from the loaded registers (X is read once); otherwise from a pass
+    // over X first.
     if (XLDS) {
-        for (int i = tid; i < MR * cpad; i += 256) {
+        const int nst = MR * cpad;  // 64-byte chunks: (m, chunk)
+        auto get = [&](int i, u32x4 (&xv)[4]) {
+            const int m = i / cpad;
+            const int c = i - m * cpad;
+            const int mm = m < p.M ? m : p.M - 1;
+#pragma unroll
+            for (int v = 0; v < 4; ++v)  // padding chunks read as x = 0
+                xv[v] = c < cpr ? *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3))
+                                : u32x4{0u, 0u, 0u, 0u};
+        };
+        auto put = [&](int i, u32x4 (&xv)[4]) {
             const int m = i / cpad;
             const int c = i - m * cpad;
             const int st = c >> 5, cl = c & 31;
@@ -222,12 +234,8 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
             float se = 0.0f, so = 0.0f;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                u32x4 xv = u32x4{0u, 0u, 0u, 0u};  // padding chunks read as x = 0
-                if (c < cpr) {
-                    xv = *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3));
-                    if (p.norm_w) xv = rms_apply8(xv, p.norm_w + (c << 5) + (v << 3), rms_inv[mm]);
-                }
-                const uint32_t xa[4] = {xv.x, xv.y, xv.z, xv.w};
+                if (p.norm_w && c < cpr) xv[v] = rms_apply8(xv[v], p.norm_w + (c << 5) + (v << 3), rms_inv[mm]);
+                const uint32_t xa[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
                 f16x2 pr[4];
                 permute_x8(xa, pr);
                 xs[((st * MR + m) * 4 + v) * 32 + cl] =
@@ -241,6 +249,34 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
             }
             // sum_k x*q = ta + tb/16 - C with ta, tb the biased dot products
             xc[(st * MR + m) * 32 + cl] = -(1032.0f * se + 72.0f * so);
+        };
+        if (p.norm_w && nst <= 512) {
+            u32x4 xv[2][4];
+            float ssm[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                if (r * 256 + tid < nst) get(r * 256 + tid, xv[r]);
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const int i = r * 256 + tid;
+                const int m = i / cpad;
+                if (i < nst && m < p.M && i - m * cpad < cpr) {
+                    const float sq = sumsq32(xv[r]);
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) ssm[q] += q == m ? sq : 0.0f;
+                }
+            }
+            rms_finish_rows<256>(ssm, p.M, K, p.norm_eps, rms_red, rms_inv);
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                if (r * 256 + tid < nst) put(r * 256 + tid, xv[r]);
+        } else {
+            if (p.norm_w) rms_inv_rows<256>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
+            for (int i = tid; i < nst; i += 256) {
+                u32x4 xv[4];
+                get(i, xv);
+                put(i, xv);
+            }
         }
     }
     __syncthreads();
@@ -523,6 +559,18 @@ const Overrides& overrides() {
 
 int mr_for(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
+}  // namespace
+
+namespace xhip_host {
+// LDS bytes of the staged X (pieces + bias terms) for MR rows and K.
+size_t gemv_x_bytes(int mr, int64_t K) { return (size_t)mr * (size_t)((K / 32 + 31) / 32) * 32 * (64 + 4); }
+// Whether the GEMV stages all of X in LDS for M rows (what an RMSNorm
+// prologue there needs).
+bool gemv_stages_x(int64_t M, int64_t K) { return gemv_x_bytes(mr_for(M), K) + 4096 <= 64 * 1024; }
+}  // namespace xhip_host
+
+namespace {
+
 // Resident blocks per CU for a kernel at a given dynamic LDS size (cached).
 int blocks_per_cu(GemvKernel k, size_t lds) {
     struct Entry { GemvKernel k; size_t lds; int dev; int v; };
@@ -592,7 +640,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
         const int cus = xhip_host::num_cus();
         int64_t total_rows = 0;
         for (int i = 0; i < p.ndesc; ++i) total_rows += p.d[i].N;
-        const size_t x_bytes = (size_t)mr * nsteps * 32 * (64 + 4);
+        const size_t x_bytes = xhip_host::gemv_x_bytes(mr, K);
         const bool xlds = x_bytes + 4096 <= 64 * 1024;
         const Overrides& ov = overrides();
         const int r = ov.r > 0 ? ov.r : (mr >= 4 && !xlds ? 1 : 2);
@@ -690,10 +738,10 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
 // 1 when the shape is left to the VALU GEMV here).
 namespace xhip_host {
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-              int64_t M, int64_t K, const float* norm_w, float eps, bool residual, int* rc);
+              int64_t M, int64_t K, bool residual, int* rc);
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
               const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
-              const float* norm_w, float eps, int* rc);
+              int* rc);
 int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts);
 int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
               int64_t M, int64_t N, int64_t K, ArgCand* parts, int* nparts, int* rc);
@@ -722,7 +770,7 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     if (M >= 2) {
         const xinfer_fused_desc one = {Y, W, S, bias, N};
         int mrc = XINFER_OK;
-        if (!mb_linear(st, &one, 1, X, y_f32, M, K, nullptr, 0.0f, residual, &mrc)) return mrc;
+        if (!mb_linear(st, &one, 1, X, y_f32, M, K, residual, &mrc)) return mrc;
     }
     GemvParams p = {};
     p.ndesc = 1;
@@ -737,21 +785,63 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     return y_f32 ? gemv_f16<EPI_PLAIN, float>(st, p, M) : gemv_f16<EPI_PLAIN, f16>(st, p, M);
 }
 
-// linear_int4_fused with an optional RMSNorm prologue on X (norm_w != null:
-// decode shapes only, M <= 8, X staged in LDS).
-int fused_f16_impl(void* stream, const void* X, const xinfer_fused_desc* descs, int32_t num_descs,
+// RMSNorm before a projection.  M = 1 (X staged whole by the GEMV): inside
+// the projection kernel, from the staged registers.  Otherwise the
+// standalone rmsnorm kernel writes the normalised rows to a per-device
+// library buffer that the projection then reads: measured faster at M >= 2
+// than a prologue inside the small-batch kernel (every block would repeat
+// the row reduction and the norm-weight reads before its first MFMA).
+// Returns the X the projection reads and whether the kernel applies the norm.
+int norm_input(hipStream_t st, const void* X, const float* norm_w, float eps, int64_t M, int64_t K,
+               const void** Xp, bool* in_kernel) {
+    *Xp = X;
+    *in_kernel = false;
+    if (!norm_w) return XINFER_OK;
+    if (M == 1 && xhip_host::gemv_stages_x(1, K)) {
+        *in_kernel = true;
+        return XINFER_OK;
+    }
+    static std::mutex mu;
+    static void* buf[64] = {nullptr};
+    static size_t cap[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return XINFER_ERR_HIP;
+    const size_t need = (size_t)M * (size_t)K * 2;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (cap[dev] < need) {  // grown, never freed: queued work may still read the old one
+            void* p = nullptr;
+            if (hipMalloc(&p, need) != hipSuccess) return XINFER_ERR_SCRATCH;
+            buf[dev] = p;
+            cap[dev] = need;
+        }
+        *Xp = buf[dev];
+    }
+    return xinfer_rmsnorm_f16(st, const_cast<void*>(*Xp), X, norm_w, M, K, eps);
+}
+
+// linear_int4_fused with an optional RMSNorm on X first (norm_w != null).
+int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs, int32_t num_descs,
                    int64_t M, int64_t K, int32_t group_size, const float* norm_w, float eps) {
     if (!descs || num_descs <= 0 || num_descs > 4) return XINFER_ERR_INVALID_ARG;
     if (M <= 0 || K <= 0) return XINFER_OK;
-    if (!X) return XINFER_ERR_INVALID_ARG;
+    if (!X0) return XINFER_ERR_INVALID_ARG;
     using namespace xhip_host;
-    if (!aligned(X, 16) || !aligned(norm_w, 4)) return XINFER_ERR_MISALIGNED;
-    if (norm_w && M > 8) return XINFER_ERR_UNSUPPORTED;
+    if (!aligned(X0, 16) || !aligned(norm_w, 4)) return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    for (int i = 0; i < num_descs; ++i) {  // shapes first: nothing is launched for a bad call
+        const xinfer_fused_desc& q = descs[i];
+        if (q.N <= 0) continue;
+        int rc = check_common(M, q.N, K, group_size);
+        if (rc) return rc;
+    }
+    const void* X = X0;
+    bool norm_in_kernel = false;
+    if (int rc = norm_input(st, X0, norm_w, eps, M, K, &X, &norm_in_kernel)) return rc;
     GemvParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
-    p.norm_w = norm_w;
+    p.norm_w = norm_in_kernel ? norm_w : nullptr;
     p.norm_eps = eps;
     xinfer_fused_desc live[4];
     int nd = 0;
@@ -780,38 +870,40 @@ int fused_f16_impl(void* stream, const void* X, const xinfer_fused_desc* descs, 
     if (M > 8 || nd == 0) return XINFER_OK;
     if (M >= 2) {
         int mrc = XINFER_OK;
-        if (!mb_linear(st, live, nd, X, false, M, K, norm_w, eps, false, &mrc)) return mrc;
+        if (!mb_linear(st, live, nd, X, false, M, K, false, &mrc)) return mrc;
     }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);
 }
 
-int swiglu_f16_impl(void* stream, void* Y, const void* X, const uint8_t* W_gate, const void* scales_gate,
+int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate, const void* scales_gate,
                     const uint8_t* W_up, const void* scales_up, int64_t M, int64_t N, int64_t K,
                     int32_t group_size, const float* norm_w, float eps) {
     if (M <= 0 || N <= 0 || K <= 0) return XINFER_OK;
     int rc = check_common(M, N, K, group_size);
     if (rc) return rc;
-    if (!Y || !X || !W_gate || !scales_gate || !W_up || !scales_up) return XINFER_ERR_INVALID_ARG;
+    if (!Y || !X0 || !W_gate || !scales_gate || !W_up || !scales_up) return XINFER_ERR_INVALID_ARG;
     using namespace xhip_host;
-    if (!aligned(W_gate, 16) || !aligned(W_up, 16) || !aligned(X, 16) || !aligned(Y, 2) ||
+    if (!aligned(W_gate, 16) || !aligned(W_up, 16) || !aligned(X0, 16) || !aligned(Y, 2) ||
         !aligned(scales_gate, 2) || !aligned(scales_up, 2) || !aligned(norm_w, 4))
         return XINFER_ERR_MISALIGNED;
-    if (norm_w && M > 8) return XINFER_ERR_UNSUPPORTED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const void* X = X0;
+    bool norm_in_kernel = false;
+    if ((rc = norm_input(st, X0, norm_w, eps, M, K, &X, &norm_in_kernel))) return rc;
     if (M > 8)
         return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
                              (const uint16_t*)scales_up, nullptr, M, N, K);
     if (M >= 2) {
         int mrc = XINFER_OK;
-        if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, norm_w, eps, &mrc))
+        if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc))
             return mrc;
     }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
-    p.norm_w = norm_w;
+    p.norm_w = norm_in_kernel ? norm_w : nullptr;
     p.norm_eps = eps;
     p.d[0].W = W_gate;
     p.d[0].S = reinterpret_cast<const uint16_t*>(scales_gate);

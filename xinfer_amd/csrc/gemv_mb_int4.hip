@@ -73,8 +73,6 @@ struct MbParams {
     int32_t tiles_blk;   // 16-row tiles per block
     int32_t nranges;     // tile ranges over all descriptors
     int32_t lkw;         // log2 of the waves that share a run of tiles, splitting its groups
-    float norm_eps;
-    const float* norm_w; // RMSNorm weight [K] applied to X while staging, or null
 };
 
 constexpr uint32_t kOutOfRange = 0xFFFFF000u;  // >= every buffer resource size used here
@@ -147,15 +145,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // LDS: X slice as MFMA A operands [group][dword t][k-quarter][m < MR] (16 B
     // each), then the block's results [wave of the run][row][m][e] (fp32:
     // one slice per wave sharing a run, summed in order), then the argmax
-    // candidates of the waves (NW values, NW indices), one flag word (padded
-    // to 16 bytes) and the RMSNorm prologue's sums and row factors.
+    // candidates of the waves (NW values, NW indices) and one flag word.
     f16x8* xs = reinterpret_cast<f16x8*>(smem);
     float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * MR * 16);
     float* candv = outl + ((size_t)p.tiles_blk * 16 * M * E << p.lkw);
     int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
     int32_t* flag = candi + NW;
-    float* rms_red = reinterpret_cast<float*>(flag + 4);  // RMSNorm sums [NW * 8], factors [8]
-    float* rms_inv = rms_red + NW * 8;
 
     // Waves come in runs of kw = 2^lkw: the waves of a run share its tiles
     // and split the slice's groups evenly (every wave gets at least one
@@ -220,9 +215,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // Stage X[:, slice] (permuted to the decode's pair order) while the
     // first weight items are in flight.  Each thread issues the loads of up
     // to kStageUnroll chunks before it waits for any, so the staging costs
-    // one memory latency instead of one per chunk round.  With an RMSNorm
-    // prologue the rows' scale factors come from the whole of K first.
-    if (p.norm_w) rms_inv_rows<NT>(p.X, M, K, p.norm_eps, rms_red, rms_inv);
+    // one memory latency instead of one per chunk round.
     {
         constexpr int kStageUnroll = 4;
         const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
@@ -247,11 +240,6 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
                     const int m = i % M;
                     const int q = i / M;
                     const int cq = q & 3, gl = q >> 2;
-                    if (p.norm_w) {
-                        const float* wk = p.norm_w + (size_t)(g0 + gl) * 128 + cq * 32;
-#pragma unroll
-                        for (int v = 0; v < 4; ++v) xv[u][v] = rms_apply8(xv[u][v], wk + 8 * v, rms_inv[m]);
-                    }
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
                         const uint32_t xa[4] = {xv[u][t].x, xv[u][t].y, xv[u][t].z, xv[u][t].w};
@@ -608,8 +596,7 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     }
     int lkw = 0;
     while ((1 << lkw) < kw) ++lkw;
-    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16 +
-                       (size_t)(nw * 8 + 8) * 4;
+    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16;
     if (lds > kMaxLds) return false;
     if (ks > 1 && ranges > (int64_t)kMaxRanges) return false;
     for (int i = 0; ks > 1 && i < p.ndesc; ++i)  // 32-bit buffer offsets into the partials
@@ -678,14 +665,12 @@ int launch_mb(const MbParams& p0, const MbPlan& pl, hipStream_t st) {
 // Entry points used by the GEMV front end (gemv_int4.hip).  Return 1 when the
 // shape is not handled here (the caller then runs the VALU GEMV).
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-              int64_t M, int64_t K, const float* norm_w, float eps, bool residual, int* rc) {
+              int64_t M, int64_t K, bool residual, int* rc) {
     MbParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.M = (int32_t)M;
     p.K = (int32_t)K;
     p.ndesc = nd;
-    p.norm_w = norm_w;
-    p.norm_eps = eps;
     for (int i = 0; i < nd; ++i) {
         p.d[i].residual = residual ? 1 : 0;
         p.d[i].W = descs[i].W_int4;
@@ -703,10 +688,8 @@ int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void
 
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
               const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
-              const float* norm_w, float eps, int* rc) {
+              int* rc) {
     MbParams p = {};
-    p.norm_w = norm_w;
-    p.norm_eps = eps;
     p.X = reinterpret_cast<const f16*>(X);
     p.M = (int32_t)M;
     p.K = (int32_t)K;

@@ -131,20 +131,54 @@ __global__ void dequant_int4_kernel(float* out, const uint8_t* W, const uint16_t
 // squares, inv = 1 / sqrt(mean + eps), out = fp16(x * inv * w).
 __global__ __launch_bounds__(256) void rmsnorm_f16_kernel(f16* out, const f16* in, const float* w,
                                                           int32_t H, float eps) {
-    __shared__ float red[4];
+    __shared__ float red[8];
+    __shared__ float inv_s[1];
     const f16* x = in + (size_t)blockIdx.x * H;
     f16* y = out + (size_t)blockIdx.x * H;
+    const int tid = threadIdx.x;
+    if ((H & 7) == 0 && ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(w) & 15) == 0) {
+        // 16-byte chunks, several loads in flight per thread in both passes
+        rms_inv_rows<256>(x, 1, H, eps, red, inv_s);
+        const float inv = inv_s[0];
+        const int c8 = H >> 3;
+        const u32x4* xr = reinterpret_cast<const u32x4*>(x);
+        const float4* wr = reinterpret_cast<const float4*>(w);
+        u32x4* yr = reinterpret_cast<u32x4*>(y);
+        for (int c0 = tid; c0 < c8; c0 += 256 * 4) {
+            u32x4 v[4];
+            float4 wa[4], wb[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * 256;
+                if (c < c8) {
+                    v[u] = xr[c];
+                    wa[u] = wr[2 * c];
+                    wb[u] = wr[2 * c + 1];
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int c = c0 + u * 256;
+                if (c < c8) {
+                    const float ww[8] = {wa[u].x, wa[u].y, wa[u].z, wa[u].w, wb[u].x, wb[u].y, wb[u].z, wb[u].w};
+                    yr[c] = rms_apply8(v[u], ww, inv);
+                }
+            }
+        }
+        return;
+    }
     float ss = 0.0f;
-    for (int i = threadIdx.x; i < H; i += 256) {
+    for (int i = tid; i < H; i += 256) {
         const float v = (float)x[i];
         ss += v * v;
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
     __syncthreads();
     const float inv = 1.0f / sqrtf((red[0] + red[1] + red[2] + red[3]) / (float)H + eps);
-    for (int i = threadIdx.x; i < H; i += 256) y[i] = (f16)((float)x[i] * inv * w[i]);
+    for (int i = tid; i < H; i += 256) y[i] = (f16)((float)x[i] * inv * w[i]);
 }
 
 // a = fp16(fp32(a) + fp32(b)) (src/ops/elementwise.cpp:213-231)
