@@ -10,6 +10,8 @@ weights rotated over enough copies (> 600 MB) that the 256 MB Infinity
 Cache cannot hold them.  Launches are replayed from a HIP graph (how a
 decode step is issued; the reference does the same with a SYCL graph,
 src/targets/qwen3_8/decode_graph.cpp), so host launch cost is not timed.
+The default warmup (8000 launches, ~0.15 s) runs the GPU into its steady
+state before the timed steps; the first ~0.1 s of work measured slower.
 
 The other BASELINE configs are measured the same way under "suite"
 (--quick skips them).  The CPU baseline is the oracle restatement of the
@@ -123,7 +125,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=640)
-    ap.add_argument("--warmup", type=int, default=64)
+    # ~0.15 s of untimed launches: the first ~0.1 s of back-to-back work on
+    # the box ran up to 8 % slower per launch (clock ramp), measured
+    ap.add_argument("--warmup", type=int, default=8000)
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,norm,crc,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")

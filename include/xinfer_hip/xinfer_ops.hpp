@@ -152,6 +152,49 @@ inline void linear_int4_naive(hipStream_t s, float* Y, const float* X, const uin
                                                                     group_size));
 }
 
+// src/ops/rmsnorm.h:17-23 (fp16 activations, fp32 weight)
+inline void rmsnorm(hipStream_t s, half* out, const half* in, const float* weight, int64_t num_tokens,
+                    int64_t hidden_size, float eps) {
+    detail::check("rmsnorm", xinfer_rmsnorm_f16(detail::q(s), out, in, weight, num_tokens, hidden_size, eps));
+}
+
+// src/ops/elementwise.h:22 (fp16)
+inline void add_inplace(hipStream_t s, half* a, const half* b, int64_t num_elements) {
+    detail::check("add_inplace", xinfer_add_inplace_f16(detail::q(s), a, b, num_elements));
+}
+
+// rmsnorm + linear_int4_fused in one call (forward.cpp:112-125, 237-247)
+inline void rmsnorm_linear_int4_fused(hipStream_t s, const half* X, const float* norm_weight, float eps,
+                                      const FusedProjectionDesc* descs, int num_descs, int64_t M,
+                                      int64_t K, int group_size = 128) {
+    auto v = detail::to_c(descs, num_descs);
+    detail::check("rmsnorm_linear_int4_fused",
+                  xinfer_rmsnorm_linear_int4_fused_f16(detail::q(s), X, norm_weight, eps,
+                                                       descs ? v.data() : nullptr, num_descs, M, K,
+                                                       group_size));
+}
+
+// rmsnorm + mlp_gate_up_swiglu_int4 in one call (forward.cpp:273-281)
+inline void rmsnorm_mlp_gate_up_swiglu_int4(hipStream_t s, half* Y, const half* X, const float* norm_weight,
+                                            float eps, const uint8_t* W_gate, const half* scales_gate,
+                                            const uint8_t* W_up, const half* scales_up, int64_t M,
+                                            int64_t N, int64_t K, int group_size = 128) {
+    detail::check("rmsnorm_mlp_gate_up_swiglu_int4",
+                  xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(detail::q(s), Y, X, norm_weight, eps, W_gate,
+                                                             scales_gate, W_up, scales_up, M, N, K,
+                                                             group_size));
+}
+
+// linear_int4 + add_inplace in one call: residual += X W^T (+ bias)
+// (forward.cpp:229/270 with :284-290)
+inline void linear_int4_residual(hipStream_t s, half* residual, const half* X, const uint8_t* W_int4,
+                                 const half* scales, const float* bias, int64_t M, int64_t N, int64_t K,
+                                 int group_size = 128) {
+    detail::check("linear_int4_residual",
+                  xinfer_linear_int4_residual_f16(detail::q(s), residual, X, W_int4, scales, bias, M, N,
+                                                  K, group_size));
+}
+
 // src/ops/sampling.h:13-17 (bytes instead of an element count)
 inline size_t argmax_scratch_size(int64_t vocab_size, int64_t rows = 1) {
     return xinfer_argmax_scratch_bytes(vocab_size, rows);

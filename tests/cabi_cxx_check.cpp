@@ -25,6 +25,27 @@ int main(int argc, char** argv) {
     } catch (const Error& e) {
         if (e.status != XINFER_ERR_INVALID_ARG) ++failures;
     }
+    // the fused neighbours of the projections: empty shapes are no-ops, bad
+    // arguments are rejected before any device work
+    rmsnorm(nullptr, nullptr, nullptr, nullptr, 0, 5120, 1e-6f);
+    add_inplace(nullptr, nullptr, nullptr, 0);
+    linear_int4_residual(nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, 16, 128);
+    try {  // rmsnorm + projection without a norm weight
+        FusedProjectionDesc d[1];
+        rmsnorm_linear_int4_fused(nullptr, (const xinfer::half*)0x1000, nullptr, 1e-6f, d, 1, 1, 128);
+        ++failures;
+    } catch (const Error& e) {
+        if (e.status != XINFER_ERR_INVALID_ARG) ++failures;
+    }
+    try {  // unsupported group size
+        rmsnorm_mlp_gate_up_swiglu_int4(nullptr, (xinfer::half*)0x1000, (const xinfer::half*)0x1000,
+                                        (const float*)0x1000, 1e-6f, (const uint8_t*)0x1000,
+                                        (const xinfer::half*)0x1000, (const uint8_t*)0x1000,
+                                        (const xinfer::half*)0x1000, 1, 16, 128, 64);
+        ++failures;
+    } catch (const Error& e) {
+        if (e.status != XINFER_ERR_UNSUPPORTED) ++failures;
+    }
     if (argmax_scratch_size(4097, 1) != 16) ++failures;
     LinearWeightView v;  // weights.h:13-23 defaults
     if (v.is_valid() || v.group_size != 128) ++failures;
