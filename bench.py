@@ -55,12 +55,14 @@ def cpu_count():
 class Rig:
     """Device buffers for one config: weight copies rotated per launch."""
 
-    def __init__(self, torch, dev, Nrows, K, sigma, seed=0):
+    def __init__(self, torch, dev, Nrows, K, sigma, seed=0, copies=None):
         from xinfer_amd import synth
         W = synth.packed_weights(seed, Nrows, K)
         S = synth.scales(seed, Nrows, K, sigma)
         one = Nrows * K // 2 + Nrows * (K // 128) * 2
         self.copies = max(2, -(-ROTATE_MIN_BYTES // one)) if one < 4 * MALL_BYTES else 2
+        if copies is not None:
+            self.copies = copies
         w0 = torch.from_numpy(W).to(dev)
         s0 = torch.from_numpy(S).view(torch.float16).to(dev)
         self.W = [w0] + [w0.clone() for _ in range(self.copies - 1)]
@@ -129,7 +131,7 @@ def main():
     # the box ran up to 8 % slower per launch (clock ramp), measured
     ap.add_argument("--warmup", type=int, default=8000)
     ap.add_argument("--quick", action="store_true", help="headline config only")
-    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,norm,crc,cfg3,cfg4")
+    ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,norm,layer,crc,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
@@ -317,6 +319,41 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
             record(f"residual_oproj_m{M}_n5120_k6144", {"M": M, "N": N, "K": K, "us_fused": round(ef * 1e6, 3),
                                                          "us_separate": round(es * 1e6, 3)})
         del rig
+
+    if want("layer"):  # one decode layer's projection sequence (forward.cpp:112-125, 229, 273-290)
+        H, Q, KV, AO, I = 5120, 12288, 1024, 6144, 17408
+        layers = []
+        for c in range(2):  # two copies (372 MB > the 256 MB Infinity Cache), alternated
+            mk = lambda i, n, k, c=c: Rig(torch, dev, n, k, 0.02, seed=10 * c + i, copies=1)  # noqa: E731
+            layers.append(dict(q=mk(0, Q, H), k=mk(1, KV, H), v=mk(2, KV, H), o=mk(3, H, AO),
+                               g=mk(4, I, H), u=mk(5, I, H), d=mk(6, H, I)))
+        lnw = [torch.linspace(0.5, 1.5, H, dtype=torch.float32, device=dev) for _ in range(2)]
+        nbytes = sum(gemv_bytes(1, r.W[0].shape[0], r.W[0].shape[1] * 2, 0, 0)
+                     for r in layers[0].values())
+        for M in (1, 4):
+            f16 = dict(dtype=torch.float16, device=dev)
+            resid = torch.from_numpy(synth.activations(0, M, H)).view(torch.float16).to(dev)
+            bq, bk, bv = (torch.empty((M, n), **f16) for n in (Q, KV, KV))
+            attn = torch.from_numpy(synth.activations(1, M, AO)).view(torch.float16).to(dev)
+            act = torch.empty((M, I), **f16)
+
+            def layer_step(i, M=M, resid=resid, bq=bq, bk=bk, bv=bv, attn=attn, act=act):
+                Lr = layers[i % 2]
+                ds = [ops.FusedProjectionDesc(Y, Lr[n].W[0], Lr[n].S[0], None, N)
+                      for Y, n, N in ((bq, "q", Q), (bk, "k", KV), (bv, "v", KV))]
+                ops.rmsnorm_linear_int4_fused(resid, lnw[0], 1e-6, ds, 3, M, H)
+                ops.linear_int4_residual(resid, attn, Lr["o"].W[0], Lr["o"].S[0], None, M, H, AO)
+                ops.rmsnorm_mlp_gate_up_swiglu_int4(act, resid, lnw[1], 1e-6, Lr["g"].W[0], Lr["g"].S[0],
+                                                    Lr["u"].W[0], Lr["u"].S[0], M, I, H)
+                ops.linear_int4_residual(resid, act, Lr["d"].W[0], Lr["d"].S[0], None, M, H, I)
+            _, eg = time_launches(torch, layer_step, 256, warm, 2, graph=True)
+            _, ee = time_launches(torch, layer_step, 256, warm, 2, graph=False)
+            record(f"decode_layer_projections_m{M}", {
+                "M": M, "launches_per_step": 4, "weight_bytes": nbytes,
+                "us_graph": round(eg * 1e6, 2), "us_eager": round(ee * 1e6, 2),
+                "GBps_graph": round(nbytes / eg / 1e9, 1),
+                "frac_hbm_graph": round(nbytes / eg / 1e9 / HBM_PEAK_GBPS, 4)})
+        del layers
 
     if want("crc"):    # .xinfer section verification on the device (GPU CRC-64)
         import ctypes
