@@ -206,77 +206,84 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
         if (++ls == nsteps) { ls = 0; ++lg; }
     };
 
+    // X staging in up to three rounds (every decode shape): its loads are
+    // issued before the weight prefetch, so the staging does not wait for
+    // the weights (loads complete in issue order).
+    const int nst = MR * cpad;  // 64-byte chunks: (m, chunk)
+    auto get = [&](int i, u32x4 (&xv)[4]) {
+        const int m = i / cpad;
+        const int c = i - m * cpad;
+        const int mm = m < p.M ? m : p.M - 1;
+#pragma unroll
+        for (int v = 0; v < 4; ++v)  // padding chunks read as x = 0
+            xv[v] = c < cpr ? *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3))
+                            : u32x4{0u, 0u, 0u, 0u};
+    };
+    auto put = [&](int i, u32x4 (&xv)[4]) {
+        const int m = i / cpad;
+        const int c = i - m * cpad;
+        const int st = c >> 5, cl = c & 31;
+        const int mm = m < p.M ? m : p.M - 1;
+        float se = 0.0f, so = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            if (p.norm_w && c < cpr) xv[v] = rms_apply8(xv[v], p.norm_w + (c << 5) + (v << 3), rms_inv[mm]);
+            const uint32_t xa[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
+            f16x2 pr[4];
+            permute_x8(xa, pr);
+            xs[((st * MR + m) * 4 + v) * 32 + cl] =
+                u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f16x2 x2 = as_h2(xa[j]);
+                se += (float)x2.x;
+                so += (float)x2.y;
+            }
+        }
+        // sum_k x*q = ta + tb/16 - C with ta, tb the biased dot products
+        xc[(st * MR + m) * 32 + cl] = -(1032.0f * se + 72.0f * so);
+    };
+    constexpr int kEarly = 3;  // staging rounds held in registers
+    const bool early = XLDS && nst <= kEarly * 256;
+    u32x4 xv0[kEarly][4];
+    if (early) {
+#pragma unroll
+        for (int r = 0; r < kEarly; ++r)
+            if (r * 256 + tid < nst) get(r * 256 + tid, xv0[r]);
+    }
+
     ItemRegs<RR> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
 
-    // zero the partial slots; stage X (permuted) and the per-chunk bias terms
+    // zero the partial slots; stage X (permuted) and the per-chunk bias terms.
+    // RMSNorm prologue: with the early staging the row sums come from the
+    // loaded registers (X is read once); otherwise from a pass over X first.
     for (int i = tid; i < nslots; i += 256) part[i] = 0.0f;
-    // RMSNorm prologue: when X is staged in at most two rounds the row sums
-    // come from the loaded registers (X is read once); otherwise from a pass
-    // over X first.
-    if (XLDS) {
-        const int nst = MR * cpad;  // 64-byte chunks: (m, chunk)
-        auto get = [&](int i, u32x4 (&xv)[4]) {
-            const int m = i / cpad;
-            const int c = i - m * cpad;
-            const int mm = m < p.M ? m : p.M - 1;
-#pragma unroll
-            for (int v = 0; v < 4; ++v)  // padding chunks read as x = 0
-                xv[v] = c < cpr ? *reinterpret_cast<const u32x4*>(p.X + (size_t)mm * K + (c << 5) + (v << 3))
-                                : u32x4{0u, 0u, 0u, 0u};
-        };
-        auto put = [&](int i, u32x4 (&xv)[4]) {
-            const int m = i / cpad;
-            const int c = i - m * cpad;
-            const int st = c >> 5, cl = c & 31;
-            const int mm = m < p.M ? m : p.M - 1;
-            float se = 0.0f, so = 0.0f;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                if (p.norm_w && c < cpr) xv[v] = rms_apply8(xv[v], p.norm_w + (c << 5) + (v << 3), rms_inv[mm]);
-                const uint32_t xa[4] = {xv[v].x, xv[v].y, xv[v].z, xv[v].w};
-                f16x2 pr[4];
-                permute_x8(xa, pr);
-                xs[((st * MR + m) * 4 + v) * 32 + cl] =
-                    u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f16x2 x2 = as_h2(xa[j]);
-                    se += (float)x2.x;
-                    so += (float)x2.y;
-                }
-            }
-            // sum_k x*q = ta + tb/16 - C with ta, tb the biased dot products
-            xc[(st * MR + m) * 32 + cl] = -(1032.0f * se + 72.0f * so);
-        };
-        if (p.norm_w && nst <= 512) {
-            u32x4 xv[2][4];
+    if (early) {
+        if (p.norm_w) {
             float ssm[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
-                if (r * 256 + tid < nst) get(r * 256 + tid, xv[r]);
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
+            for (int r = 0; r < kEarly; ++r) {
                 const int i = r * 256 + tid;
                 const int m = i / cpad;
                 if (i < nst && m < p.M && i - m * cpad < cpr) {
-                    const float sq = sumsq32(xv[r]);
+                    const float sq = sumsq32(xv0[r]);
 #pragma unroll
                     for (int q = 0; q < 8; ++q) ssm[q] += q == m ? sq : 0.0f;
                 }
             }
             rms_finish_rows<256>(ssm, p.M, K, p.norm_eps, rms_red, rms_inv);
+        }
 #pragma unroll
-            for (int r = 0; r < 2; ++r)
-                if (r * 256 + tid < nst) put(r * 256 + tid, xv[r]);
-        } else {
-            if (p.norm_w) rms_inv_rows<256>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
-            for (int i = tid; i < nst; i += 256) {
-                u32x4 xv[4];
-                get(i, xv);
-                put(i, xv);
-            }
+        for (int r = 0; r < kEarly; ++r)
+            if (r * 256 + tid < nst) put(r * 256 + tid, xv0[r]);
+    } else if (XLDS) {
+        if (p.norm_w) rms_inv_rows<256>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
+        for (int i = tid; i < nst; i += 256) {
+            u32x4 xv[4];
+            get(i, xv);
+            put(i, xv);
         }
     }
     __syncthreads();
