@@ -207,49 +207,53 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
         }
     };
 
+    // Stage X[:, slice] (permuted to the decode's pair order).  The loads of
+    // the first round (up to kStageUnroll chunks per thread) are issued
+    // before the weight prefetch: loads complete in issue order, so the
+    // staging then waits for X alone while the weight items stay in flight.
+    constexpr int kStageUnroll = 4;
+    const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
+    auto get = [&](int i, u32x4 (&xv)[4]) {
+        const int m = i % M;
+        const int q = i / M;
+        const u32x4* src = reinterpret_cast<const u32x4*>(
+            p.X + (size_t)m * K + (size_t)(g0 + (q >> 2)) * 128 + (q & 3) * 32);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xv[v] = src[v];
+    };
+    auto put = [&](int i, const u32x4 (&xv)[4]) {
+        const int m = i % M;
+        const int q = i / M;
+        const int cq = q & 3, gl = q >> 2;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t xa[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
+            f16x2 pr[4];
+            permute_x8(xa, pr);
+            xs[((gl * 4 + t) * 4 + cq) * MR + m] = pack_q8(pr);
+        }
+    };
+    u32x4 xv0[kStageUnroll][4];
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u)
+        if (tid + u * NT < chunks) get(tid + u * NT, xv0[u]);
+
     constexpr int PF = XHIP_MB_PF;  // items in flight per wave
     MbItem<E> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
 
-    // Stage X[:, slice] (permuted to the decode's pair order) while the
-    // first weight items are in flight.  Each thread issues the loads of up
-    // to kStageUnroll chunks before it waits for any, so the staging costs
-    // one memory latency instead of one per chunk round.
-    {
-        constexpr int kStageUnroll = 4;
-        const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
-        for (int i0 = tid; i0 < chunks; i0 += NT * kStageUnroll) {
-            u32x4 xv[kStageUnroll][4];
 #pragma unroll
-            for (int u = 0; u < kStageUnroll; ++u) {
-                const int i = i0 + u * NT;
-                if (i < chunks) {
-                    const int m = i % M;
-                    const int q = i / M;
-                    const u32x4* src = reinterpret_cast<const u32x4*>(
-                        p.X + (size_t)m * K + (size_t)(g0 + (q >> 2)) * 128 + (q & 3) * 32);
+    for (int u = 0; u < kStageUnroll; ++u)
+        if (tid + u * NT < chunks) put(tid + u * NT, xv0[u]);
+    for (int i0 = tid + NT * kStageUnroll; i0 < chunks; i0 += NT * kStageUnroll) {  // further rounds
+        u32x4 xv[kStageUnroll][4];
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) xv[u][v] = src[v];
-                }
-            }
+        for (int u = 0; u < kStageUnroll; ++u)
+            if (i0 + u * NT < chunks) get(i0 + u * NT, xv[u]);
 #pragma unroll
-            for (int u = 0; u < kStageUnroll; ++u) {
-                const int i = i0 + u * NT;
-                if (i < chunks) {
-                    const int m = i % M;
-                    const int q = i / M;
-                    const int cq = q & 3, gl = q >> 2;
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t xa[4] = {xv[u][t].x, xv[u][t].y, xv[u][t].z, xv[u][t].w};
-                        f16x2 pr[4];
-                        permute_x8(xa, pr);
-                        xs[((gl * 4 + t) * 4 + cq) * MR + m] = pack_q8(pr);
-                    }
-                }
-            }
-        }
+        for (int u = 0; u < kStageUnroll; ++u)
+            if (i0 + u * NT < chunks) put(i0 + u * NT, xv[u]);
     }
     __syncthreads();  // X staged
 
