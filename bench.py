@@ -433,7 +433,15 @@ def cpu_baseline(nbytes, log):
         log(f"  cpu oracle {threads} thread(s): {dt*1e3:.1f} ms/step, {reps} reps")
     cores = cpu_count()
     v, dt, reps = res[cores]
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    log(f"  cpu: {model} ({os.cpu_count()} logical cpus on the host, {cores} used)")
     return {"value": round(v, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "cpu_model": model, "host_nproc": os.cpu_count(),
             "sample": f"full config-1 step (M=1, K=5120, 2x17408 rows) x {reps} reps, "
                       f"OpenMP over {cores} threads; single-thread: "
                       f"{res[1][0]:.3f} GB/s ({res[1][1]*1e3:.0f} ms/step)",
