@@ -34,6 +34,7 @@
 
 #include <stdlib.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "common.h"
@@ -583,8 +584,10 @@ int blocks_per_cu(GemvKernel k, size_t lds) {
     struct Entry { GemvKernel k; size_t lds; int dev; int v; };
     static Entry cache[256];
     static int n = 0;
+    static std::mutex mu;
     int dev = 0;
     (void)hipGetDevice(&dev);
+    std::lock_guard<std::mutex> lock(mu);
     for (int i = 0; i < n; ++i)
         if (cache[i].k == k && cache[i].lds == lds && cache[i].dev == dev) return cache[i].v;
     int v = 0;
@@ -712,16 +715,16 @@ int check_common(int64_t M, int64_t N, int64_t K, int32_t G) {
 namespace xhip_host {
 
 int num_cus() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
-        int v = 0;
+    int v = cached[dev].load(std::memory_order_relaxed);
+    if (!v) {
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0)
             v = 256;
-        cached[dev] = v;
+        cached[dev].store(v, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return v;
 }
 
 int launch_status() { return hipGetLastError() == hipSuccess ? XINFER_OK : XINFER_ERR_HIP; }

@@ -549,11 +549,16 @@ struct MbPlan {
 //        that measured slower (each wave then decodes fewer groups per
 //        fixed prologue).
 //   MR:  the m stride of the staged X (4 for M <= 4, else 8).
+bool gemv_stages_x(int64_t M, int64_t K);  // gemv_int4.hip
+
 template <int EPI, typename OutT>
 bool plan_mb(MbParams& p, MbPlan& pl) {
     const MbOverrides& ov = mb_overrides();
     const int M = p.M;
-    const int min_m = ov.min_m > 0 ? ov.min_m : 3;  // M = 2: the VALU GEMV measured faster
+    // M = 2: the VALU GEMV measured faster while it stages all of X in LDS
+    // (K = 5120: 8.1 vs 8.2 us, N = 34816: 19.3 vs 27.3 us); beyond that its
+    // global-X path is slower than this kernel (K = 17408: 20.3 vs 14.5 us)
+    const int min_m = ov.min_m > 0 ? ov.min_m : gemv_stages_x(2, p.K) ? 3 : 2;
     if (M < min_m || M < 2 || M > 8) return false;
     const int E = EPI == MB_SWIGLU ? 2 : 1;
     const int ng = p.K / 128;
