@@ -199,3 +199,58 @@ def test_lm_head_back_to_back_calls():
             got = to_np(ids)
             for m in range(M):
                 assert got[m] == oracle.argmax(ref[m]), (M, call, m)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 1000, 1024), (16, 4096, 5120), (17, 333, 2048), (33, 2000, 5120),
+                                   (64, 5120, 17408), (48, 17408, 5120)])
+def test_chunk_rows_m9_to_64(M, N, K):
+    """Chunked-prefill row counts: 9..16 fill the small-batch kernel's 16-row
+    MFMA tile (exact FP32 scaling: fp32 outputs within 1e-4), 17..64 run the
+    MFMA GEMM (q*s rounded to fp16: fp32 outputs held to the fp16 bound).
+    Plain fp16, fp32 with bias, residual."""
+    import torch
+    ops = _ops()
+    print("case", M, N, K, flush=True)
+    W, S, Xb = _inputs(M * 3 + N, M, N, K)
+    dW, dS, dX = to_dev(W), f16_dev(S), f16_dev(Xb)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+    Y = _empty((M, N), torch.float16)
+    ops.linear_int4(Y, dX, dW, dS, None, M, N, K)
+    print(check_f16_tol(to_np(Y), ref))
+    bias = np.linspace(-2, 2, N).astype(np.float32)
+    Yf = _empty((M, N), torch.float32)
+    ops.linear_int4(Yf, dX, dW, dS, to_dev(bias), M, N, K)
+    if M <= 16:
+        _check_f32(to_np(Yf), ref + bias)
+    else:
+        err = np.abs(to_np(Yf) - (ref + bias)).max()
+        assert err <= 1e-2 and kat.rel_l2(to_np(Yf), ref + bias) <= 1e-3, err
+    R = f16_dev(oracle.f32_to_f16(np.full((M, N), 0.5, np.float32)))
+    ops.linear_int4_residual(R, dX, dW, dS, None, M, N, K)
+    want = oracle.add_inplace_f16(oracle.f32_to_f16(np.full((M, N), 0.5, np.float32)), to_np(Y))
+    assert np.array_equal(to_np(R), want)
+
+
+@pytest.mark.parametrize("M", [12, 40])
+def test_chunk_rows_swiglu_and_fused(M):
+    import torch
+    ops = _ops()
+    K = 2048
+    Xb = synth.activations(50 + M, M, K)
+    X = oracle.f16_to_f32(Xb)
+    N = 1500
+    Wg, Wu = synth.packed_weights(5, N, K), synth.packed_weights(5, N, K, synth.STREAM_W2)
+    Sg, Su = synth.scales(5, N, K), synth.scales(5, N, K, stream=synth.STREAM_S2)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), to_dev(Wg), f16_dev(Sg), to_dev(Wu), f16_dev(Su), M, N, K)
+    print(check_f16_tol(to_np(Y), oracle.swiglu_int4(X, Wg, Sg, Wu, Su, M, N, K, nthreads=cpu_threads())))
+    descs, refs, outs = [], [], []
+    for p, n in enumerate((384, 128, 48)):
+        W, S = synth.packed_weights(60 + p, n, K), synth.scales(60 + p, n, K)
+        refs.append(oracle.linear_int4(X, W, S, M, n, K))
+        Yd = _empty((M, n), torch.float16)
+        outs.append(Yd)
+        descs.append(ops.FusedProjectionDesc(Yd, to_dev(W), f16_dev(S), None, n))
+    ops.linear_int4_fused(f16_dev(Xb), descs, 3, M, K)
+    for Yd, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Yd), ref))

@@ -753,6 +753,7 @@ int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const v
               const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
               int* rc);
 int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts);
+int mb_max_m();  // largest M the small-batch kernel takes (then the GEMM)
 int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
               int64_t M, int64_t N, int64_t K, ArgCand* parts, int* nparts, int* rc);
 int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
@@ -774,14 +775,14 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
         !aligned(bias, 4))
         return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-    if (M > 8)
-        return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K,
-                             residual);
-    if (M >= 2) {
+    if (M >= 2 && M <= mb_max_m()) {
         const xinfer_fused_desc one = {Y, W, S, bias, N};
         int mrc = XINFER_OK;
         if (!mb_linear(st, &one, 1, X, y_f32, M, K, residual, &mrc)) return mrc;
     }
+    if (M > 8)
+        return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K,
+                             residual);
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);
@@ -863,12 +864,6 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
         if (!q.Y || !q.W_int4 || !q.scales) return XINFER_ERR_INVALID_ARG;
         if (!aligned(q.W_int4, 16) || !aligned(q.scales, 2) || !aligned(q.Y, 2) || !aligned(q.bias, 4))
             return XINFER_ERR_MISALIGNED;
-        if (M > 8) {
-            rc = gemm_int4_f16(st, q.Y, false, X, q.W_int4, (const uint16_t*)q.scales, nullptr,
-                               nullptr, q.bias, M, q.N, K);
-            if (rc) return rc;
-            continue;
-        }
         live[nd] = q;
         GemvDesc& g = p.d[nd++];
         g.W = q.W_int4;
@@ -877,10 +872,19 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
         g.Y = q.Y;
         g.N = (int32_t)q.N;
     }
-    if (M > 8 || nd == 0) return XINFER_OK;
-    if (M >= 2) {
+    if (nd == 0) return XINFER_OK;
+    if (M >= 2 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
         if (!mb_linear(st, live, nd, X, false, M, K, false, &mrc)) return mrc;
+    }
+    if (M > 8) {  // one GEMM per descriptor
+        for (int i = 0; i < nd; ++i) {
+            const xinfer_fused_desc& q = live[i];
+            const int rc = gemm_int4_f16(st, q.Y, false, X, q.W_int4, (const uint16_t*)q.scales, nullptr,
+                                         nullptr, q.bias, M, q.N, K);
+            if (rc) return rc;
+        }
+        return XINFER_OK;
     }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);
@@ -901,14 +905,14 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
     const void* X = X0;
     bool norm_in_kernel = false;
     if ((rc = norm_input(st, X0, norm_w, eps, M, K, &X, &norm_in_kernel))) return rc;
-    if (M > 8)
-        return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
-                             (const uint16_t*)scales_up, nullptr, M, N, K);
-    if (M >= 2) {
+    if (M >= 2 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
         if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc))
             return mrc;
     }
+    if (M > 8)
+        return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
+                             (const uint16_t*)scales_up, nullptr, M, N, K);
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);

@@ -66,7 +66,7 @@ struct MbParams {
     int64_t ws_desc[4];  // float offset of each descriptor's partials in ws
     int32_t ws_slice[4]; // floats per k-slice of each descriptor (multiple of 64: 256-byte aligned)
     int32_t ndesc;
-    int32_t M;           // 2..8
+    int32_t M;           // 2..8 (argmax), 2..64 otherwise
     int32_t K;
     int32_t ks;          // k-slices per tile range
     int32_t gps;         // groups per k-slice (the last slice may be shorter)
@@ -473,7 +473,10 @@ MbKernel mb_pick_nw(int nw) {
 
 template <int EPI, typename OutT>
 MbKernel mb_kernel_for(int mr, int nw) {
-    return mr <= 4 ? mb_pick_nw<4, EPI, OutT>(nw) : mb_pick_nw<8, EPI, OutT>(nw);
+    if (mr <= 4) return mb_pick_nw<4, EPI, OutT>(nw);
+    if (mr <= 8 || EPI == MB_ARGMAX) return mb_pick_nw<8, EPI, OutT>(nw);  // the LM head: M <= 8
+    if constexpr (EPI != MB_ARGMAX) return mb_pick_nw<16, EPI, OutT>(nw);
+    return nullptr;
 }
 
 int env_int(const char* name, int dflt) {
@@ -493,6 +496,12 @@ const MbOverrides& mb_overrides() {
 }
 
 constexpr size_t kMaxLds = 160 * 1024;
+// Chunked-prefill rows 9..16 fill the 16-row MFMA tile (N = 17408,
+// K = 5120: 21.6 / 25.1 us at M = 9 / 16 against 47 / 48 us for the GEMM,
+// whose 128-row tiles are mostly padding there).  Two to four M-tiles per
+// weight tile (M = 17..64) measured slower than the GEMM: the X slice of
+// 32-64 rows forces 5-10 k-slices and a large split-K combine.
+constexpr int kMaxMbM = 16;
 
 // Per-device workspace for split-K partial sums plus a zeroed counter array.
 // Grown on demand (outside any graph capture: the first call of a shape
@@ -548,7 +557,7 @@ struct MbPlan {
 //        shapes without a cross-block combine; more waves per tile than
 //        that measured slower (each wave then decodes fewer groups per
 //        fixed prologue).
-//   MR:  the m stride of the staged X (4 for M <= 4, else 8).
+//   MR:  the m stride of the staged X (4, 8 or 16: M rounded up).
 bool gemv_stages_x(int64_t M, int64_t K);  // gemv_int4.hip
 
 template <int EPI, typename OutT>
@@ -559,15 +568,15 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     // (K = 5120: 8.1 vs 8.2 us, N = 34816: 19.3 vs 27.3 us); beyond that its
     // global-X path is slower than this kernel (K = 17408: 20.3 vs 14.5 us)
     const int min_m = ov.min_m > 0 ? ov.min_m : gemv_stages_x(2, p.K) ? 3 : 2;
-    if (M < min_m || M < 2 || M > 8) return false;
+    if (M < min_m || M < 2 || M > (EPI == MB_ARGMAX ? 8 : kMaxMbM)) return false;
     const int E = EPI == MB_SWIGLU ? 2 : 1;
     const int ng = p.K / 128;
     const int cus = num_cus();
     int64_t tiles_total = 0;
     for (int i = 0; i < p.ndesc; ++i) tiles_total += (p.d[i].N + 15) / 16;
-    const int mr = M <= 4 ? 4 : 8;
+    const int mr = M <= 4 ? 4 : M <= 8 ? 8 : 16;
     const size_t xg = (size_t)mr * 256;  // LDS bytes of X per group
-    const size_t x_budget = EPI == MB_ARGMAX ? 96 * 1024 : 48 * 1024;
+    const size_t x_budget = EPI == MB_ARGMAX ? 96 * 1024 : mr >= 16 ? 64 * 1024 : 48 * 1024;
     int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
     if (EPI == MB_ARGMAX) ks = 1;
     if (ks > ng) ks = ng;
@@ -726,6 +735,14 @@ int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts) {
     if (!plan_mb<MB_ARGMAX, float>(p, pl)) return 1;
     *nparts = pl.nranges;
     return 0;
+}
+
+int mb_max_m() {
+    static const int v = [] {
+        const int o = env_int("XINFER_MB_MAX_M", 0);
+        return o > 0 ? (o < kMaxMbM ? o : kMaxMbM) : kMaxMbM;
+    }();
+    return v;
 }
 
 int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
