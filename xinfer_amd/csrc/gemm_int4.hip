@@ -27,6 +27,8 @@
 //   * epilogue: bias / fp16 or fp32 store, or SiLU(gate) * up when the block
 //     holds paired gate and up tiles (SwiGLU prefill).
 
+#include <stdlib.h>
+
 #include <mutex>
 
 #include "common.h"
@@ -366,21 +368,34 @@ size_t gemm_lds_bytes(int nt) {
 template <int EPI, typename OutT>
 int launch_gemm(hipStream_t st, GemmParams& p) {
     // Candidate N tiles (16-column MFMA tiles per block).  Estimated time =
-    // rounds of one-block-per-CU waves x work per block.
+    // rounds of one-block-per-CU waves x the measured time of one block of
+    // that configuration (N = 17408, K = 5120 on MI355X: 17 tiles with the
+    // leftover tile 110 us, 16 tiles 91 us, 8 tiles 60 us, 4 leftover-only
+    // tiles 125 us; the leftover tile's extra A read makes 17 tiles cost more
+    // than 16/17 of them would suggest).
     const int cus = xhip_host::num_cus();
     const GemmCfg cands_plain[] = {{2, 1}, {2, 0}, {1, 0}, {0, 4}};
+    const double block_cost_plain[] = {1.21, 1.0, 0.66, 1.37};
     const GemmCfg cands_swiglu[] = {{1, 0}};
     const GemmCfg* cands = EPI == 1 ? cands_swiglu : cands_plain;
     const int ncand = EPI == 1 ? 1 : 4;
     const int mblocks = (p.M + kGM - 1) / kGM;
     GemmCfg best = cands[0];
     double best_cost = 1e300;
+    static const int forced = [] {  // XINFER_GEMM_CFG: candidate index (tuning only)
+        const char* v = getenv("XINFER_GEMM_CFG");
+        return (v && *v) ? atoi(v) : -1;
+    }();
     for (int i = 0; i < ncand; ++i) {
+        if (forced >= 0 && forced < ncand) {
+            best = cands[forced];
+            break;
+        }
         const int nt = EPI == 1 ? kWavesG * cands[i].nq : kWavesG * cands[i].nq + cands[i].nr;
         const int64_t nranges = (p.N + 16 * nt - 1) / (16 * nt);
         const int64_t blocks = mblocks * nranges;
         const int64_t rounds = (blocks + cus - 1) / cus;
-        const double cost = (double)rounds * nt * (1.0 + 0.5 / nt);  // + per-block overhead
+        const double cost = (double)rounds * (EPI == 1 ? 1.0 : block_cost_plain[i]);
         if (cost < best_cost) { best_cost = cost; best = cands[i]; }
     }
     const int nt_w = EPI == 1 ? 2 * kWavesG * best.nq : kWavesG * best.nq + best.nr;  // weight tiles
