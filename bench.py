@@ -10,8 +10,9 @@ weights rotated over enough copies (> 600 MB) that the 256 MB Infinity
 Cache cannot hold them.  Launches are replayed from a HIP graph (how a
 decode step is issued; the reference does the same with a SYCL graph,
 src/targets/qwen3_8/decode_graph.cpp), so host launch cost is not timed.
-The default warmup (8000 launches, ~0.15 s) runs the GPU into its steady
-state before the timed steps; the first ~0.1 s of work measured slower.
+Every timing first runs the GPU into its steady state: the requested warmup
+launches, and at least 0.1 s of back-to-back launches (the first ~0.1 s of
+work after an idle period measured up to 8 % slower per launch).
 
 The other BASELINE configs are measured the same way under "suite"
 (--quick skips them).  The CPU baseline is the oracle restatement of the
@@ -69,9 +70,17 @@ class Rig:
         self.S = [s0] + [s0.clone() for _ in range(self.copies - 1)]
 
 
+MIN_WARM_S = 0.1  # the GPU reaches its steady clock after ~0.1 s of back-to-back work
+
+
 def _time_eager(torch, launch, steps, warmup, copies):
-    for i in range(warmup):
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or time.perf_counter() - t0 < MIN_WARM_S:
         launch(i % copies)
+        i += 1
+        if i % 64 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -97,8 +106,13 @@ def _time_graph(torch, launch, steps, warmup, copies):
             for i in range(per):
                 launch(i % copies)
     reps = max(1, steps // per)
-    for _ in range(max(1, warmup // per)):
+    t0 = time.perf_counter()
+    r = 0
+    while r < max(1, warmup // per) or time.perf_counter() - t0 < MIN_WARM_S:
         g.replay()
+        r += 1
+        if r % 8 == 0:
+            torch.cuda.synchronize()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

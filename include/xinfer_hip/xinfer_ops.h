@@ -55,9 +55,11 @@ const char* xinfer_version(void);
 /* ---------------------------------------------------------------------------
  * linear_int4: Y[m][n] = sum_g fp32(S[n][g]) * sum_{j<128} X[m][128g+j] *
  *              q[n][128g+j] (+ bias[n]), FP32 accumulation.
- * M <= 8 runs the bandwidth-bound GEMV kernels; larger M (chunked prefill)
- * runs the MFMA GEMM, as the reference routes both through this one call
- * (src/targets/qwen3_8/forward.cpp:284-287).
+ * M <= 16 runs the bandwidth-bound decode kernels (VALU GEMV at M = 1-2,
+ * MFMA small-batch kernel at M = 2-16); larger M (chunked prefill) runs the
+ * MFMA GEMM, as the reference routes both through this one call
+ * (src/targets/qwen3_8/forward.cpp:284-287).  The fp32-output GEMM rounds
+ * q*s to fp16 once per weight (the decode kernels scale in FP32).
  * ------------------------------------------------------------------------- */
 
 /* Replaces `sycl::event linear_int4(sycl::queue&, sycl::half* Y,
