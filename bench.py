@@ -21,6 +21,7 @@ reference CPU loop, timed on this host's cores.
     python bench.py                       # default: N=1, all configs
     python bench.py --only cfg1 --no-cpu  # one config (profiling runs)
     python bench.py --calib-copy          # plain copy of known size (PMC scale)
+    python bench.py --calib-dense-gemm    # hipBLASLt fp16 GEMM at the config 4 shape
 """
 from __future__ import annotations
 
@@ -150,6 +151,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 256 MiB device copy 20x (PMC calibration) and exit")
+    ap.add_argument("--calib-dense-gemm", action="store_true",
+                    help="time torch.matmul (hipBLASLt) fp16 X @ W^T at the config 4 shape and exit")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -174,6 +177,24 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log(f"copied {n} bytes x 20")
+        return
+
+    if args.calib_dense_gemm:
+        # Reference point for the prefill GEMM: the vendor library's dense
+        # fp16 GEMM (no dequantisation) at the same shape and weight layout
+        # ([N][K], row-major), weights rotated past the Infinity Cache.
+        M, N, K = 512, 17408, 5120
+        copies = max(1, -(-ROTATE_MIN_BYTES // (N * K * 2)))
+        X = torch.randn(M, K, dtype=torch.float16, device=dev)
+        Ws = [torch.randn(N, K, dtype=torch.float16, device=dev) for _ in range(copies)]
+        Y = torch.empty(M, N, dtype=torch.float16, device=dev)
+        fn = lambda i: torch.matmul(X, Ws[i].t(), out=Y)  # noqa: E731
+        w, e = time_launches(torch, fn, args.steps, args.warmup // 20, copies, graph=True)
+        tf = 2.0 * M * N * K / e / 1e12
+        print(json.dumps({"calib": "dense_fp16_gemm_hipblaslt", "M": M, "N": N, "K": K,
+                          "us": round(e * 1e6, 2), "TFLOPs": round(tf, 1),
+                          "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
+                          "weight_copies": copies}))
         return
 
     only = set(x for x in args.only.split(",") if x)
