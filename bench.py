@@ -259,7 +259,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic,
-                     "kernel": "xhip::gemv_int4_kernel<MR=1,R=2,EPI_SWIGLU,...,PF=1>",
+                     "kernel": "xhip::gemv_int4_kernel<MR=1,R=2,EPI_SWIGLU,...,PF=1,NWV=8>",
                      "algorithmic_bytes_per_launch": nbytes,
                      "avg_launch_us": round(ev_step * 1e6, 3)},
         "cpu_baseline": cpu,

@@ -3,10 +3,10 @@
 // Replaces the reference's sub-group GEMV family (src/ops/linear.cpp:33-163
 // split-K, 165-305 main, 351-498 fused, 501-617 SwiGLU) with one MI355X
 // design:
-//   * a fixed grid of a few 256-thread blocks per CU; each block owns a
-//     contiguous range of output rows.  Its work is a list of items
-//     (group of 2R rows, 1024-k step) in row-major order, cut into 4 equal
-//     contiguous pieces, one per wave.  Small N therefore splits K across
+//   * a fixed grid of one or two blocks per CU (8 waves at M = 1, else 4);
+//     each block owns a contiguous range of output rows.  Its work is a list
+//     of items (group of 2R rows, 1024-k step) in row-major order, cut into
+//     equal contiguous pieces, one per wave.  Small N therefore splits K across
 //     waves by itself (the reference's split-K).  Items are wave-uniform, so
 //     all item bookkeeping and row addresses live in SGPRs.
 //   * in an item, half-wave h covers rows 2R*g + h*R .. + R - 1; lane j of
@@ -67,11 +67,11 @@ struct GemvParams {
     int32_t K;
 };
 
-constexpr int kWaves = 4;  // waves per 256-thread block
-// dynamic LDS in front of the X pieces: RMSNorm partial sums (kWaves * 8)
-// and the row factors (8), padded to keep the pieces 16-byte aligned
-constexpr int kGemvLdsHead = 256;
-static_assert((kWaves * 8 + 8) * 4 <= kGemvLdsHead, "RMSNorm scratch");
+// dynamic LDS in front of the X pieces: RMSNorm partial sums (8 per wave,
+// up to 8 waves) and the row factors (8), padded to keep the pieces 16-byte
+// aligned
+constexpr int kGemvLdsHead = 512;
+static_assert((8 * 8 + 8) * 4 <= kGemvLdsHead, "RMSNorm scratch for up to 8 waves");
 
 template <int RR>
 struct ItemRegs {
@@ -107,8 +107,9 @@ __device__ __forceinline__ void decode16_biased(uint32_t w0, uint32_t w1, f16x2 
     h[7] = as_h2((b8 & 0x00F000F0u) ^ 0x64806480u);
 }
 
-template <int MR, int R, int EPI, typename OutT, bool XLDS, int PF>
-__global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
+template <int MR, int R, int EPI, typename OutT, bool XLDS, int PF, int NWV>
+__global__ __launch_bounds__(64 * NWV) void gemv_int4_kernel(const GemvParams p) {
+    constexpr int NTH = 64 * NWV;                        // threads per block
     constexpr int RR = (EPI == EPI_SWIGLU) ? 2 * R : R;  // weight rows per half-wave item
     constexpr int E = (EPI == EPI_SWIGLU) ? 2 : 1;       // sums per output
     constexpr int G2 = 2 * R;                            // output rows per item
@@ -144,15 +145,15 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
     // The first kGemvLdsHead bytes hold the RMSNorm prologue's reduction.
     const int cpad = nsteps * 32;
     float* rms_red = reinterpret_cast<float*>(smem);
-    float* rms_inv = rms_red + kWaves * 8;
+    float* rms_inv = rms_red + NWV * 8;
     u32x4* xs = reinterpret_cast<u32x4*>(smem + kGemvLdsHead);
     float* xc = reinterpret_cast<float*>(smem + kGemvLdsHead + (size_t)(XLDS ? MR * 4 * cpad : 0) * 16);
     float* part = xc + (XLDS ? MR * cpad : 0);
     const int nslots = d.rows_blk * MR * E * nsteps;
 
     const int items = groups * nsteps;
-    const int it0 = (wave * items) / kWaves;
-    const int it1 = ((wave + 1) * items) / kWaves;
+    const int it0 = (wave * items) / NWV;
+    const int it1 = ((wave + 1) * items) / NWV;
 
     const uint8_t* Wb0 = d.W;
     const uint16_t* Sb0 = d.S;
@@ -245,12 +246,12 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
         xc[(st * MR + m) * 32 + cl] = -(1032.0f * se + 72.0f * so);
     };
     constexpr int kEarly = 3;  // staging rounds held in registers
-    const bool early = XLDS && nst <= kEarly * 256;
+    const bool early = XLDS && nst <= kEarly * NTH;
     u32x4 xv0[kEarly][4];
     if (early) {
 #pragma unroll
         for (int r = 0; r < kEarly; ++r)
-            if (r * 256 + tid < nst) get(r * 256 + tid, xv0[r]);
+            if (r * NTH + tid < nst) get(r * NTH + tid, xv0[r]);
     }
 
     ItemRegs<RR> buf[PF + 1];
@@ -260,13 +261,13 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
     // zero the partial slots; stage X (permuted) and the per-chunk bias terms.
     // RMSNorm prologue: with the early staging the row sums come from the
     // loaded registers (X is read once); otherwise from a pass over X first.
-    for (int i = tid; i < nslots; i += 256) part[i] = 0.0f;
+    for (int i = tid; i < nslots; i += NTH) part[i] = 0.0f;
     if (early) {
         if (p.norm_w) {
             float ssm[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int r = 0; r < kEarly; ++r) {
-                const int i = r * 256 + tid;
+                const int i = r * NTH + tid;
                 const int m = i / cpad;
                 if (i < nst && m < p.M && i - m * cpad < cpr) {
                     const float sq = sumsq32(xv0[r]);
@@ -274,14 +275,14 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
                     for (int q = 0; q < 8; ++q) ssm[q] += q == m ? sq : 0.0f;
                 }
             }
-            rms_finish_rows<256>(ssm, p.M, K, p.norm_eps, rms_red, rms_inv);
+            rms_finish_rows<NTH>(ssm, p.M, K, p.norm_eps, rms_red, rms_inv);
         }
 #pragma unroll
         for (int r = 0; r < kEarly; ++r)
-            if (r * 256 + tid < nst) put(r * 256 + tid, xv0[r]);
+            if (r * NTH + tid < nst) put(r * NTH + tid, xv0[r]);
     } else if (XLDS) {
-        if (p.norm_w) rms_inv_rows<256>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
-        for (int i = tid; i < nst; i += 256) {
+        if (p.norm_w) rms_inv_rows<NTH>(p.X, p.M, K, p.norm_eps, rms_red, rms_inv);
+        for (int i = tid; i < nst; i += NTH) {
             u32x4 xv[4];
             get(i, xv);
             put(i, xv);
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
     if (EPI == EPI_ARGMAX) {
         float bv = -__builtin_inff();
         int32_t bi = 0x7FFFFFFF;
-        for (int o = tid; o < nout; o += 256) {
+        for (int o = tid; o < nout; o += NTH) {
             const int rl = o / MR, m = o - rl * MR;
             float v = 0.0f;
             for (int s = 0; s < nsteps; ++s) v += part[(rl * MR + m) * nsteps + s];
@@ -428,7 +429,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
         }
         __syncthreads();  // partial slots are reused for the candidates below
         float* cv = part;
-        int32_t* ci = reinterpret_cast<int32_t*>(part + kWaves * MR);
+        int32_t* ci = reinterpret_cast<int32_t*>(part + NWV * MR);
         if (lane < MR) {
             cv[wave * MR + lane] = bv;
             ci[wave * MR + lane] = bi;
@@ -437,7 +438,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
         if (tid < MR && tid < p.M) {
             float b = cv[tid];
             int32_t i = ci[tid];
-            for (int w = 1; w < kWaves; ++w)
+            for (int w = 1; w < NWV; ++w)
                 if (arg_better(cv[w * MR + tid], ci[w * MR + tid], b, i)) { b = cv[w * MR + tid]; i = ci[w * MR + tid]; }
             ArgCand o;
             o.v = b;
@@ -445,7 +446,7 @@ __global__ __launch_bounds__(256) void gemv_int4_kernel(const GemvParams p) {
             p.parts[(size_t)tid * gridDim.x + blockIdx.x] = o;
         }
     } else {
-        for (int o = tid; o < nout; o += 256) {
+        for (int o = tid; o < nout; o += NTH) {
             const int rl = o / MR, m = o - rl * MR;
             if (m >= p.M) continue;
             const int n = row_begin + rl;
@@ -513,7 +514,7 @@ namespace {
 
 
 struct GemvPlan {
-    int mr, r, pf, blocks;
+    int mr, r, pf, blocks, nw;
     bool xlds;
     size_t lds;
 };
@@ -521,33 +522,36 @@ struct GemvPlan {
 typedef void (*GemvKernel)(GemvParams);
 
 template <int MR, int R, int EPI, typename OutT, int PF>
-GemvKernel pick_kernel(bool xlds) {
-    return xlds ? gemv_int4_kernel<MR, R, EPI, OutT, true, PF>
-                : gemv_int4_kernel<MR, R, EPI, OutT, false, PF>;
+GemvKernel pick_kernel(bool xlds, int nw) {
+    // M = 1 with R = 2 runs 8-wave blocks (gemv_waves), everything else 4
+    constexpr int NWV = (MR == 1 && R == 2) ? 8 : 4;
+    (void)nw;
+    return xlds ? gemv_int4_kernel<MR, R, EPI, OutT, true, PF, NWV>
+                : gemv_int4_kernel<MR, R, EPI, OutT, false, PF, NWV>;
 }
 
 template <int MR, int R, int EPI, typename OutT>
-GemvKernel pick_pf(bool xlds, int pf) {
+GemvKernel pick_pf(bool xlds, int pf, int nw) {
     if (MR == 1 && EPI != EPI_ARGMAX) {
-        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds);
-        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
-        return pick_kernel<MR, R, EPI, OutT, 3>(xlds);
+        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds, nw);
+        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds, nw);
+        return pick_kernel<MR, R, EPI, OutT, 3>(xlds, nw);
     }
-    return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
+    return pick_kernel<MR, R, EPI, OutT, 2>(xlds, nw);
 }
 
 template <int EPI, typename OutT>
-GemvKernel kernel_for(int mr, int r, bool xlds, int pf) {
+GemvKernel kernel_for(int mr, int r, bool xlds, int pf, int nw) {
     switch (mr) {
         case 1:
-            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf)
-                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf) : pick_pf<1, 4, EPI, OutT>(xlds, pf);
+            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf, nw)
+                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf, nw) : pick_pf<1, 4, EPI, OutT>(xlds, pf, nw);
         case 2:
-            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf) : pick_pf<2, 4, EPI, OutT>(xlds, pf);
+            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf, nw) : pick_pf<2, 4, EPI, OutT>(xlds, pf, nw);
         case 4:
-            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf) : pick_pf<4, 2, EPI, OutT>(xlds, pf);
+            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf, nw) : pick_pf<4, 2, EPI, OutT>(xlds, pf, nw);
         default:
-            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf) : pick_pf<8, 2, EPI, OutT>(xlds, pf);
+            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf, nw) : pick_pf<8, 2, EPI, OutT>(xlds, pf, nw);
     }
 }
 
@@ -565,6 +569,12 @@ const Overrides& overrides() {
     return o;
 }
 
+// Waves per block: 8 for M = 1 with two rows per half-wave (X staged once
+// for twice the waves), 4 otherwise.  Measured on MI355X, graph-replayed:
+// config 1 17.97 -> 17.45 us, q-proj 6.00 -> 5.70, down-proj (K = 17408)
+// 12.77 -> 11.05, LM head 65.2 -> 64.5, north-star 17.3 -> 17.4.
+int gemv_waves(int mr, int r) { return (mr == 1 && r == 2) ? 8 : 4; }
+
 int mr_for(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
 }  // namespace
@@ -580,7 +590,7 @@ bool gemv_stages_x(int64_t M, int64_t K) { return gemv_x_bytes(mr_for(M), K) + 4
 namespace {
 
 // Resident blocks per CU for a kernel at a given dynamic LDS size (cached).
-int blocks_per_cu(GemvKernel k, size_t lds) {
+int blocks_per_cu(GemvKernel k, size_t lds, int threads) {
     struct Entry { GemvKernel k; size_t lds; int dev; int v; };
     static Entry cache[256];
     static int n = 0;
@@ -591,7 +601,7 @@ int blocks_per_cu(GemvKernel k, size_t lds) {
     for (int i = 0; i < n; ++i)
         if (cache[i].k == k && cache[i].lds == lds && cache[i].dev == dev) return cache[i].v;
     int v = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(k), 256, lds) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(k), threads, lds) !=
             hipSuccess || v <= 0)
         v = 1;
     if (v > 8) v = 8;
@@ -655,10 +665,13 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
         const Overrides& ov = overrides();
         const int r = ov.r > 0 ? ov.r : (mr >= 4 && !xlds ? 1 : 2);
         const int pf = ov.pf > 0 ? ov.pf : (mr == 1 ? 1 : 2);
-        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf);
+        const int nw = gemv_waves(mr, r);
+        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf, nw);
         int64_t rows = 0;
         size_t lds = 0;
-        int bpc = ov.bpc > 0 ? ov.bpc : 2;
+        // 8-wave blocks: two per CU, one when X is long (each block stages
+        // all of X, and at K = 17408 that staging delays the weight stream)
+        int bpc = ov.bpc > 0 ? ov.bpc : (nw == 4 ? 2 : (xlds && x_bytes > 24 * 1024) ? 1 : 2);
         for (int pass = 0; pass < 3; ++pass) {
             const int64_t target = (int64_t)cus * bpc;
             rows = (total_rows + target - 1) / target;
@@ -669,16 +682,36 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
             if (lds <= 64 * 1024) break;
             bpc *= 2;  // smaller row ranges until the partial slots fit
         }
-        const int occ = blocks_per_cu(k, lds);
+        const int occ = blocks_per_cu(k, lds, 64 * nw);
+        auto lds_for = [&](int64_t rr) {
+            size_t part = (size_t)rr * mr * E * nsteps * 4;
+            if (EPI == EPI_ARGMAX && part < 2048) part = 2048;
+            return kGemvLdsHead + (xlds ? x_bytes : 0) + part;
+        };
         if (ov.bpc <= 0 && occ < bpc) {  // cannot hold the target residency
             const int64_t target = (int64_t)cus * occ;
             int64_t r2 = (total_rows + target - 1) / target;
             r2 = ((r2 + 2 * r - 1) / (2 * r)) * (2 * r);
-            if (kGemvLdsHead + (size_t)r2 * mr * E * nsteps * 4 + (xlds ? x_bytes : 0) <= 64 * 1024) rows = r2;
+            if (lds_for(r2) <= 64 * 1024) rows = r2;
+        }
+        // Each descriptor rounds its block count up, so several descriptors
+        // can overshoot the resident grid by a block or two, which would then
+        // run as a second wave on its own (fused QKV at M = 1: 513 blocks for
+        // 512 slots).  Grow the rows per block until the grid is resident.
+        if (ov.bpc <= 0) {
+            const int64_t slots = (int64_t)cus * occ;
+            for (int it = 0; it < 64; ++it) {
+                int64_t nb = 0;
+                for (int i = 0; i < p.ndesc; ++i) nb += (p.d[i].N + rows - 1) / rows;
+                if (nb <= slots || lds_for(rows + 2 * r) > 64 * 1024) break;
+                rows += 2 * r;
+            }
+            lds = lds_for(rows);
         }
         best.mr = mr;
         best.r = r;
         best.pf = pf;
+        best.nw = nw;
         best.xlds = xlds;
         best.lds = lds;
         rows_blk = (int32_t)rows;
@@ -698,8 +731,8 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
 
 template <int EPI, typename OutT>
 void launch_plan(const GemvParams& p, const GemvPlan& pl, hipStream_t st) {
-    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf);
-    hipLaunchKernelGGL(k, dim3(pl.blocks), dim3(256), pl.lds, st, p);
+    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf, pl.nw);
+    hipLaunchKernelGGL(k, dim3(pl.blocks), dim3(64 * pl.nw), pl.lds, st, p);
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int32_t G) {
