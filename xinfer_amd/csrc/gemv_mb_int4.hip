@@ -576,11 +576,18 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     for (int i = 0; i < p.ndesc; ++i) tiles_total += (p.d[i].N + 15) / 16;
     const int mr = M <= 4 ? 4 : M <= 8 ? 8 : 16;
     const size_t xg = (size_t)mr * 256;  // LDS bytes of X per group
-    const size_t x_budget = EPI == MB_ARGMAX ? 96 * 1024 : mr >= 16 ? 64 * 1024 : 48 * 1024;
+    size_t x_budget = EPI == MB_ARGMAX ? 96 * 1024 : mr >= 16 ? 64 * 1024 : 48 * 1024;
+    // Long K at an 8-row stride (X over four 48 KB slices): 96 KB slices,
+    // still 4 waves.  Measured at K = 17408, N = 5120: M = 5 20.1 -> 16.3 us,
+    // M = 8 21.6 -> 18.0 (3 slices instead of 6).  At K <= 6144 the larger
+    // slices leave one block per CU and lose (gate/up M = 8 42.1 -> 45.7 us).
+    const bool long_k8 = EPI != MB_ARGMAX && mr == 8 && (size_t)ng * xg > 4 * 48 * 1024;
+    if (long_k8) x_budget = 96 * 1024;
     int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
     if (EPI == MB_ARGMAX) ks = 1;
     if (ks > ng) ks = ng;
-    int nw = ov.nw > 0 ? ov.nw : ((size_t)ng * xg / ks > 64 * 1024 ? 8 : 4);
+    const size_t nw_at = long_k8 ? 96 * 1024 : 64 * 1024;  // X slice beyond this: 8 waves
+    int nw = ov.nw > 0 ? ov.nw : ((size_t)ng * xg / ks > nw_at ? 8 : 4);
     nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
     const int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
     const int64_t target = (int64_t)cus * bpc;
