@@ -523,8 +523,8 @@ typedef void (*GemvKernel)(GemvParams);
 
 template <int MR, int R, int EPI, typename OutT, int PF>
 GemvKernel pick_kernel(bool xlds, int nw) {
-    // M = 1 with R = 2 runs 8-wave blocks (gemv_waves), everything else 4
-    constexpr int NWV = (MR == 1 && R == 2) ? 8 : 4;
+    // M <= 2 with R = 2 runs 8-wave blocks (gemv_waves), everything else 4
+    constexpr int NWV = (MR <= 2 && R == 2) ? 8 : 4;
     (void)nw;
     return xlds ? gemv_int4_kernel<MR, R, EPI, OutT, true, PF, NWV>
                 : gemv_int4_kernel<MR, R, EPI, OutT, false, PF, NWV>;
@@ -569,11 +569,24 @@ const Overrides& overrides() {
     return o;
 }
 
-// Waves per block: 8 for M = 1 with two rows per half-wave (X staged once
-// for twice the waves), 4 otherwise.  Measured on MI355X, graph-replayed:
-// config 1 17.97 -> 17.45 us, q-proj 6.00 -> 5.70, down-proj (K = 17408)
-// 12.77 -> 11.05, LM head 65.2 -> 64.5, north-star 17.3 -> 17.4.
-int gemv_waves(int mr, int r) { return (mr == 1 && r == 2) ? 8 : 4; }
+// Waves per block: 8 for M <= 2 with two rows per half-wave (X staged once
+// for twice the waves), 4 otherwise.  Measured on MI355X, graph-replayed
+// (M = 1): config 1 17.97 -> 17.45 us, q-proj 6.00 -> 5.70, down-proj
+// (K = 17408) 12.77 -> 11.05, LM head 65.2 -> 64.5, north-star 17.3 -> 17.4.
+int gemv_waves(int mr, int r) { return (mr <= 2 && r == 2) ? 8 : 4; }
+
+// 8-wave blocks run one per CU once their staged X passes 12 KB (each block
+// stages all of X, which delays its weight stream), else two.  Measured,
+// graph-replayed: down-proj K = 17408 M = 1 11.7 -> 11.0 us, o_proj K = 6144
+// M = 1 6.5 -> 5.9, q-proj K = 5120 M = 2 8.5 -> 7.6; at K = 5120 M = 1
+// (11 KB) two blocks stay better (q-proj 5.7 vs 6.0).
+bool gemv_one_block_per_cu(int nw, size_t x_bytes) { return nw == 8 && x_bytes > 12 * 1024; }
+
+// LDS a GEMV block may use: a block alone on its CU may take the CU's
+// 160 KB; otherwise 64 KB keeps two or more blocks resident.
+size_t gemv_lds_cap(int nw, size_t x_bytes) {
+    return gemv_one_block_per_cu(nw, x_bytes) ? 159 * 1024 : 64 * 1024;
+}
 
 int mr_for(int64_t M) { return M <= 1 ? 1 : M <= 2 ? 2 : M <= 4 ? 4 : 8; }
 
@@ -584,10 +597,31 @@ namespace xhip_host {
 size_t gemv_x_bytes(int mr, int64_t K) { return (size_t)mr * (size_t)((K / 32 + 31) / 32) * 32 * (64 + 4); }
 // Whether the GEMV stages all of X in LDS for M rows (what an RMSNorm
 // prologue there needs).
-bool gemv_stages_x(int64_t M, int64_t K) { return gemv_x_bytes(mr_for(M), K) + 4096 <= 64 * 1024; }
+bool gemv_stages_x(int64_t M, int64_t K) {
+    const int mr = mr_for(M);
+    const size_t xb = gemv_x_bytes(mr, K);
+    return xb + 4096 <= gemv_lds_cap(gemv_waves(mr, 2), xb);
+}
 }  // namespace xhip_host
 
 namespace {
+
+// Allow a kernel more than the default 64 KB of dynamic LDS (once per
+// kernel; the attribute must be set before such a launch).
+bool allow_lds(GemvKernel k, size_t lds) {
+    if (lds <= 64 * 1024) return true;
+    static std::mutex mu;
+    static GemvKernel done[64];
+    static int n = 0;
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < n; ++i)
+        if (done[i] == k) return true;
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(k), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            160 * 1024) != hipSuccess)
+        return false;
+    if (n < 64) done[n++] = k;
+    return true;
+}
 
 // Resident blocks per CU for a kernel at a given dynamic LDS size (cached).
 int blocks_per_cu(GemvKernel k, size_t lds, int threads) {
@@ -661,17 +695,17 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
         int64_t total_rows = 0;
         for (int i = 0; i < p.ndesc; ++i) total_rows += p.d[i].N;
         const size_t x_bytes = xhip_host::gemv_x_bytes(mr, K);
-        const bool xlds = x_bytes + 4096 <= 64 * 1024;
         const Overrides& ov = overrides();
-        const int r = ov.r > 0 ? ov.r : (mr >= 4 && !xlds ? 1 : 2);
+        const bool xlds_std = x_bytes + 4096 <= 64 * 1024;
+        const int r = ov.r > 0 ? ov.r : (mr >= 4 && !xlds_std ? 1 : 2);
+        const size_t lds_cap = gemv_lds_cap(gemv_waves(mr, r), x_bytes);
+        const bool xlds = x_bytes + 4096 <= lds_cap;
         const int pf = ov.pf > 0 ? ov.pf : (mr == 1 ? 1 : 2);
         const int nw = gemv_waves(mr, r);
         GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf, nw);
         int64_t rows = 0;
         size_t lds = 0;
-        // 8-wave blocks: two per CU, one when X is long (each block stages
-        // all of X, and at K = 17408 that staging delays the weight stream)
-        int bpc = ov.bpc > 0 ? ov.bpc : (nw == 4 ? 2 : (xlds && x_bytes > 24 * 1024) ? 1 : 2);
+        int bpc = ov.bpc > 0 ? ov.bpc : (xlds && gemv_one_block_per_cu(nw, x_bytes)) ? 1 : 2;
         for (int pass = 0; pass < 3; ++pass) {
             const int64_t target = (int64_t)cus * bpc;
             rows = (total_rows + target - 1) / target;
@@ -679,9 +713,10 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
             size_t part = (size_t)rows * mr * E * nsteps * 4;
             if (EPI == EPI_ARGMAX && part < 2048) part = 2048;
             lds = kGemvLdsHead + (xlds ? x_bytes : 0) + part;
-            if (lds <= 64 * 1024) break;
+            if (lds <= lds_cap) break;
             bpc *= 2;  // smaller row ranges until the partial slots fit
         }
+        (void)allow_lds(k, lds);  // before the occupancy query; checked again at launch
         const int occ = blocks_per_cu(k, lds, 64 * nw);
         auto lds_for = [&](int64_t rr) {
             size_t part = (size_t)rr * mr * E * nsteps * 4;
@@ -692,7 +727,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
             const int64_t target = (int64_t)cus * occ;
             int64_t r2 = (total_rows + target - 1) / target;
             r2 = ((r2 + 2 * r - 1) / (2 * r)) * (2 * r);
-            if (lds_for(r2) <= 64 * 1024) rows = r2;
+            if (lds_for(r2) <= lds_cap) rows = r2;
         }
         // Each descriptor rounds its block count up, so several descriptors
         // can overshoot the resident grid by a block or two, which would then
@@ -703,7 +738,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
             for (int it = 0; it < 64; ++it) {
                 int64_t nb = 0;
                 for (int i = 0; i < p.ndesc; ++i) nb += (p.d[i].N + rows - 1) / rows;
-                if (nb <= slots || lds_for(rows + 2 * r) > 64 * 1024) break;
+                if (nb <= slots || lds_for(rows + 2 * r) > lds_cap) break;
                 rows += 2 * r;
             }
             lds = lds_for(rows);
@@ -730,9 +765,11 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
 }
 
 template <int EPI, typename OutT>
-void launch_plan(const GemvParams& p, const GemvPlan& pl, hipStream_t st) {
+int launch_plan(const GemvParams& p, const GemvPlan& pl, hipStream_t st) {
     GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf, pl.nw);
+    if (!allow_lds(k, pl.lds)) return XINFER_ERR_HIP;
     hipLaunchKernelGGL(k, dim3(pl.blocks), dim3(64 * pl.nw), pl.lds, st, p);
+    return XINFER_OK;
 }
 
 int check_common(int64_t M, int64_t N, int64_t K, int32_t G) {
@@ -770,7 +807,7 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
     const GemvPlan pl = plan_gemv<EPI, OutT>(p, mr_for(M));
     if (pl.blocks <= 0) return XINFER_OK;
     if (p.norm_w && !pl.xlds) return XINFER_ERR_UNSUPPORTED;  // the prologue runs while staging X
-    launch_plan<EPI, OutT>(p, pl, st);
+    if (launch_plan<EPI, OutT>(p, pl, st)) return XINFER_ERR_HIP;
     return launch_status();
 }
 
@@ -1084,8 +1121,7 @@ extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* log
         return XINFER_ERR_SCRATCH;
     }
     p.parts = reinterpret_cast<ArgCand*>(scratch);
-    launch_plan<EPI_ARGMAX, float>(p, pl, st);
-    if (launch_status()) return XINFER_ERR_HIP;
+    if (launch_plan<EPI_ARGMAX, float>(p, pl, st) || launch_status()) return XINFER_ERR_HIP;
     hipLaunchKernelGGL((argmax_finalize_kernel<int32_t>), dim3((unsigned)M), dim3(256), 0, st,
                        p.parts, (int32_t)blocks, ids);
     return launch_status();
