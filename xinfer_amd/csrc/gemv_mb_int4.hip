@@ -586,10 +586,18 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
     if (EPI == MB_ARGMAX) ks = 1;
     if (ks > ng) ks = ng;
-    const size_t nw_at = long_k8 ? 96 * 1024 : 64 * 1024;  // X slice beyond this: 8 waves
-    int nw = ov.nw > 0 ? ov.nw : ((size_t)ng * xg / ks > nw_at ? 8 : 4);
+    const size_t slice = (size_t)ng * xg / ks;
+    // X slice beyond nw_at: 8 waves.  The LM head keeps 4 waves at one block
+    // per CU (M = 8, N = 151936: 94.0 -> 89.5 us against 8 waves).
+    const size_t nw_at = long_k8 ? 96 * 1024 : 64 * 1024;
+    int nw = ov.nw > 0 ? ov.nw : (EPI != MB_ARGMAX && slice > nw_at) ? 8 : 4;
     nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
-    const int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
+    int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
+    // never plan more blocks per CU than their X slices leave resident
+    if (ov.bpc <= 0) {
+        const int fit = (int)(kMaxLds / (slice + 4096));
+        if (fit < bpc) bpc = fit < 1 ? 1 : fit;
+    }
     const int64_t target = (int64_t)cus * bpc;
     int64_t tiles_blk = 0, ranges = 0;
     for (int pass = 0; pass < 2; ++pass) {
