@@ -203,6 +203,31 @@ def test_ragged_shapes_m1(N, K):
     print(_linear_case(2, N, K, seed=N, out="f32"))
 
 
+# Long K: the M <= 2 GEMV stages X in more than 64 KB of LDS (one 8-wave
+# block per CU); past three staging rounds it stages in a loop; past 159 KB
+# M = 2 runs the small-batch kernel.
+@pytest.mark.parametrize("M,N,K", [(1, 520, 40960), (1, 300, 74240), (2, 260, 30720), (2, 200, 40960)])
+def test_long_k_large_lds(M, N, K):
+    print(_linear_case(M, N, K, seed=K % 97))
+
+
+def test_long_k_swiglu_m1():
+    import torch
+    ops = _ops()
+    M, N, K = 1, 264, 40960
+    # scales |N(0, 0.005)|/7 keep |y| below 4 at this K (with config 1's 0.02
+    # the outputs reach ~36, where fp16 spacing alone exceeds the 1e-2 bound)
+    W = synth.packed_weights(3, 2 * N, K)
+    S = synth.scales(3, 2 * N, K, 0.005)
+    Xb = synth.activations(3, M, K)
+    dW, dS = to_dev(W), f16_dev(S)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), dW[:N], dS[:N], dW[N:], dS[N:], M, N, K)
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb), W[:N], S[:N], W[N:], S[N:], M, N, K,
+                             nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y), ref))
+
+
 def test_bias_is_added():
     import torch
     ops = _ops()
