@@ -522,36 +522,35 @@ struct GemvPlan {
 typedef void (*GemvKernel)(GemvParams);
 
 template <int MR, int R, int EPI, typename OutT, int PF>
-GemvKernel pick_kernel(bool xlds, int nw) {
+GemvKernel pick_kernel(bool xlds) {
     // M <= 2 with R = 2 runs 8-wave blocks (gemv_waves), everything else 4
     constexpr int NWV = (MR <= 2 && R == 2) ? 8 : 4;
-    (void)nw;
     return xlds ? gemv_int4_kernel<MR, R, EPI, OutT, true, PF, NWV>
                 : gemv_int4_kernel<MR, R, EPI, OutT, false, PF, NWV>;
 }
 
 template <int MR, int R, int EPI, typename OutT>
-GemvKernel pick_pf(bool xlds, int pf, int nw) {
+GemvKernel pick_pf(bool xlds, int pf) {
     if (MR == 1 && EPI != EPI_ARGMAX) {
-        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds, nw);
-        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds, nw);
-        return pick_kernel<MR, R, EPI, OutT, 3>(xlds, nw);
+        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds);
+        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
+        return pick_kernel<MR, R, EPI, OutT, 3>(xlds);
     }
-    return pick_kernel<MR, R, EPI, OutT, 2>(xlds, nw);
+    return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
 }
 
 template <int EPI, typename OutT>
-GemvKernel kernel_for(int mr, int r, bool xlds, int pf, int nw) {
+GemvKernel kernel_for(int mr, int r, bool xlds, int pf) {
     switch (mr) {
         case 1:
-            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf, nw)
-                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf, nw) : pick_pf<1, 4, EPI, OutT>(xlds, pf, nw);
+            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf)
+                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf) : pick_pf<1, 4, EPI, OutT>(xlds, pf);
         case 2:
-            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf, nw) : pick_pf<2, 4, EPI, OutT>(xlds, pf, nw);
+            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf) : pick_pf<2, 4, EPI, OutT>(xlds, pf);
         case 4:
-            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf, nw) : pick_pf<4, 2, EPI, OutT>(xlds, pf, nw);
+            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf) : pick_pf<4, 2, EPI, OutT>(xlds, pf);
         default:
-            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf, nw) : pick_pf<8, 2, EPI, OutT>(xlds, pf, nw);
+            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf) : pick_pf<8, 2, EPI, OutT>(xlds, pf);
     }
 }
 
@@ -702,7 +701,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
         const bool xlds = x_bytes + 4096 <= lds_cap;
         const int pf = ov.pf > 0 ? ov.pf : (mr == 1 ? 1 : 2);
         const int nw = gemv_waves(mr, r);
-        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf, nw);
+        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf);
         int64_t rows = 0;
         size_t lds = 0;
         int bpc = ov.bpc > 0 ? ov.bpc : (xlds && gemv_one_block_per_cu(nw, x_bytes)) ? 1 : 2;
@@ -766,7 +765,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
 
 template <int EPI, typename OutT>
 int launch_plan(const GemvParams& p, const GemvPlan& pl, hipStream_t st) {
-    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf, pl.nw);
+    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf);
     if (!allow_lds(k, pl.lds)) return XINFER_ERR_HIP;
     hipLaunchKernelGGL(k, dim3(pl.blocks), dim3(64 * pl.nw), pl.lds, st, p);
     return XINFER_OK;
