@@ -21,7 +21,7 @@ reference CPU loop, timed on this host's cores.
     python bench.py                       # default: N=1, all configs
     python bench.py --only cfg1 --no-cpu  # one config (profiling runs)
     python bench.py --calib-copy          # plain copy of known size (PMC scale)
-    python bench.py --calib-dense-gemm    # hipBLASLt fp16 GEMM at the config 4 shape
+    python bench.py --calib-dense-gemm    # hipBLASLt fp16 GEMM at the config 4 shape and two others
 """
 from __future__ import annotations
 
@@ -180,21 +180,24 @@ def main():
         return
 
     if args.calib_dense_gemm:
-        # Reference point for the prefill GEMM: the vendor library's dense
-        # fp16 GEMM (no dequantisation) at the same shape and weight layout
-        # ([N][K], row-major), weights rotated past the Infinity Cache.
-        M, N, K = 512, 17408, 5120
-        copies = max(1, -(-ROTATE_MIN_BYTES // (N * K * 2)))
-        X = torch.randn(M, K, dtype=torch.float16, device=dev)
-        Ws = [torch.randn(N, K, dtype=torch.float16, device=dev) for _ in range(copies)]
-        Y = torch.empty(M, N, dtype=torch.float16, device=dev)
-        fn = lambda i: torch.matmul(X, Ws[i].t(), out=Y)  # noqa: E731
-        w, e = time_launches(torch, fn, args.steps, args.warmup // 20, copies, graph=True)
-        tf = 2.0 * M * N * K / e / 1e12
-        print(json.dumps({"calib": "dense_fp16_gemm_hipblaslt", "M": M, "N": N, "K": K,
-                          "us": round(e * 1e6, 2), "TFLOPs": round(tf, 1),
-                          "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
-                          "weight_copies": copies}))
+        # Reference points for the prefill GEMM: the vendor library's dense
+        # fp16 GEMM (no dequantisation) in the same weight layout ([N][K],
+        # row-major), weights rotated past the Infinity Cache: the config 4
+        # shape, twice its M, and a large square GEMM.
+        for M, N, K in ((512, 17408, 5120), (1024, 17408, 5120), (8192, 8192, 8192)):
+            copies = max(1, -(-ROTATE_MIN_BYTES // (N * K * 2)))
+            X = torch.randn(M, K, dtype=torch.float16, device=dev)
+            Ws = [torch.randn(N, K, dtype=torch.float16, device=dev) for _ in range(copies)]
+            Y = torch.empty(M, N, dtype=torch.float16, device=dev)
+            fn = lambda i, X=X, Ws=Ws, Y=Y: torch.matmul(X, Ws[i].t(), out=Y)  # noqa: E731
+            steps = max(copies, min(args.steps, int(2e13 // (2 * M * N * K))))
+            w, e = time_launches(torch, fn, steps, max(copies, args.warmup // 20), copies, graph=True)
+            tf = 2.0 * M * N * K / e / 1e12
+            print(json.dumps({"calib": "dense_fp16_gemm_hipblaslt", "M": M, "N": N, "K": K,
+                              "us": round(e * 1e6, 2), "TFLOPs": round(tf, 1),
+                              "frac_fp16_mfma": round(tf / FP16_PEAK_TFLOPS, 4),
+                              "weight_copies": copies}), flush=True)
+            del X, Ws, Y
         return
 
     only = set(x for x in args.only.split(",") if x)
