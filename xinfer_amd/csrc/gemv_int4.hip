@@ -379,25 +379,37 @@ __global__ __launch_bounds__(64 * NWV) void gemv_int4_kernel(const GemvParams p)
     };
 
     // compute cursor (group, step); a run of one group starts at step run0.
-    // The ring loop has no branches around loads (exact vmcnt tracking); the
-    // item count is padded to a multiple of PF + 1 with zero items.
+    // The ring loop's body has no branch around a load (exact vmcnt
+    // tracking); loads it issues for items past the end read zeros and are
+    // never waited on.
     int cg = it0 / nsteps;
     int cs = it0 - cg * nsteps;
     int run0 = cs;
     const int nreal = it1 - it0;
-    for (int base = 0; base < nreal; base += PF + 1) {
+    auto retire = [&](int k) {  // item k computed: close its run when the run ends
+        if (++cs == nsteps || k + 1 == nreal) {
+            flush(cg, run0);
+            if (cs == nsteps) { cs = 0; ++cg; }
+            run0 = cs;
+        }
+    };
+    int base = 0;
+    for (; base + PF + 1 <= nreal; base += PF + 1) {
 #pragma unroll
         for (int j = 0; j <= PF; ++j) {
-            const int k = base + j;
             load_next(buf[(j + PF) % (PF + 1)]);
             compute_item(min(cs, nsteps - 1), buf[j]);
-            if (k < nreal) {
-                if (++cs == nsteps || k + 1 == nreal) {
-                    flush(cg, run0);
-                    if (cs == nsteps) { cs = 0; ++cg; }
-                    run0 = cs;
-                }
-            }
+            retire(base + j);
+        }
+    }
+    // the last nreal - base (<= PF) items are already in the ring: compute
+    // them without issuing or waiting on loads for items past the end
+    // (waiting on such padding loads cost ~1 us at the end of a wave)
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        if (base + j < nreal) {
+            compute_item(min(cs, nsteps - 1), buf[j]);
+            retire(base + j);
         }
     }
     __syncthreads();
