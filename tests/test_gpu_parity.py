@@ -228,6 +228,44 @@ def test_long_k_swiglu_m1():
     print(check_f16_tol(to_np(Y), ref))
 
 
+# M = 1 launches of at least 32768 rows (K = 4096..6144) run the row-pair
+# kernel: bias, fp32 output, the residual epilogue, several descriptors, and
+# an odd N (left to the GEMV).
+@pytest.mark.parametrize("N,K,out", [(32768, 4096, "f16"), (34816, 6144, "f32"), (33000, 5120, "f16"),
+                                     (32769, 5120, "f16")])
+def test_pair_kernel_shapes(N, K, out):
+    print(_linear_case(1, N, K, seed=N % 89, out=out))
+
+
+def test_pair_kernel_bias_residual_descs():
+    import torch
+    ops = _ops()
+    K = 5120
+    Xb = synth.activations(21, 1, K)
+    X = oracle.f16_to_f32(Xb)
+    # bias + residual on one 32768-row projection
+    N = 32768
+    W, S = synth.packed_weights(21, N, K), synth.scales(21, N, K)
+    bias = np.linspace(-0.5, 0.5, N).astype(np.float32)
+    r0 = synth.activations(22, 1, N)
+    R = f16_dev(r0)
+    ops.linear_int4_residual(R, f16_dev(Xb), to_dev(W), f16_dev(S), to_dev(bias), 1, N, K)
+    ref = oracle.linear_int4(X, W, S, 1, N, K, bias=bias, nthreads=cpu_threads())
+    print(check_f16_tol(to_np(R), oracle.f16_to_f32(r0).astype(np.float64) + ref))
+    # four descriptors, 33792 rows together, pair boundaries inside each
+    Ns = (12288, 10240, 6146, 5118)
+    descs, outs, refs = [], [], []
+    for p, Np in enumerate(Ns):
+        Wp, Sp = synth.packed_weights(30 + p, Np, K), synth.scales(30 + p, Np, K)
+        refs.append(oracle.linear_int4(X, Wp, Sp, 1, Np, K, nthreads=cpu_threads()))
+        Y = _empty((1, Np), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(Wp), f16_dev(Sp), None, Np))
+    ops.linear_int4_fused(f16_dev(Xb), descs, 4, 1, K)
+    for Y, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Y), ref))
+
+
 def test_bias_is_added():
     import torch
     ops = _ops()

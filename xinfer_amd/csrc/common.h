@@ -51,6 +51,26 @@ __device__ __forceinline__ void permute_x8(const uint32_t x[4], f16x2 p[4]) {
     p[3] = as_h2(__builtin_amdgcn_perm(x[3], x[1], 0x07060302u));  // (x3, x7)
 }
 
+// Biased decode of 16 nibbles (two dwords, natural nibble order) into 8 fp16
+// pairs of exact integers 1024 + u or 1024 + 16u (u = q + 8), in the pair
+// order permute_x8 gives the activations; the caller removes the bias per
+// 32-k chunk (sum x*q = ta + tb/16 - C).
+// Two dwords at once: one 64-bit shift provides the ">> 8" of both
+// (bits 24-31 of the low result hold bits of the high dword, but only bits
+// 0-7 and 16-23 survive the masks).
+__device__ __forceinline__ void decode16_biased(uint32_t w0, uint32_t w1, f16x2 h[8]) {
+    const uint64_t w8 = (((uint64_t)w1 << 32) | w0) >> 8;
+    const uint32_t a8 = (uint32_t)w8, b8 = (uint32_t)(w8 >> 32);
+    h[0] = as_h2((w0 & 0x000F000Fu) ^ 0x64086408u);
+    h[1] = as_h2((w0 & 0x00F000F0u) ^ 0x64806480u);
+    h[2] = as_h2((a8 & 0x000F000Fu) ^ 0x64086408u);
+    h[3] = as_h2((a8 & 0x00F000F0u) ^ 0x64806480u);
+    h[4] = as_h2((w1 & 0x000F000Fu) ^ 0x64086408u);
+    h[5] = as_h2((w1 & 0x00F000F0u) ^ 0x64806480u);
+    h[6] = as_h2((b8 & 0x000F000Fu) ^ 0x64086408u);
+    h[7] = as_h2((b8 & 0x00F000F0u) ^ 0x64806480u);
+}
+
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }
@@ -208,5 +228,11 @@ inline bool aligned(const void* p, uintptr_t a) {
 
 int num_cus();                 // compute units of the current device (cached)
 int launch_status();           // XINFER_OK or XINFER_ERR_HIP after a launch
+// Row-pair GEMV for large M = 1 projections (gemv_pair_int4.hip): whether it
+// takes a launch, and the launch (returns 1 when the shape is left to the
+// GEMV, else 0 with *rc the launch status).
+bool pair_takes(int64_t M, int64_t K, int64_t n_total);
+int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
+                int64_t K, bool residual, int* rc);
 
 }  // namespace xhip_host

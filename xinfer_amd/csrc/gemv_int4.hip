@@ -91,22 +91,6 @@ __device__ __forceinline__ void decode8_biased(uint32_t w, f16x2 h[4]) {
     h[3] = as_h2((w8 & 0x00F000F0u) ^ 0x64806480u);
 }
 
-// Two dwords at once: one 64-bit shift provides the ">> 8" of both
-// (bits 24-31 of the low result hold bits of the high dword, but only bits
-// 0-7 and 16-23 survive the masks).
-__device__ __forceinline__ void decode16_biased(uint32_t w0, uint32_t w1, f16x2 h[8]) {
-    const uint64_t w8 = (((uint64_t)w1 << 32) | w0) >> 8;
-    const uint32_t a8 = (uint32_t)w8, b8 = (uint32_t)(w8 >> 32);
-    h[0] = as_h2((w0 & 0x000F000Fu) ^ 0x64086408u);
-    h[1] = as_h2((w0 & 0x00F000F0u) ^ 0x64806480u);
-    h[2] = as_h2((a8 & 0x000F000Fu) ^ 0x64086408u);
-    h[3] = as_h2((a8 & 0x00F000F0u) ^ 0x64806480u);
-    h[4] = as_h2((w1 & 0x000F000Fu) ^ 0x64086408u);
-    h[5] = as_h2((w1 & 0x00F000F0u) ^ 0x64806480u);
-    h[6] = as_h2((b8 & 0x000F000Fu) ^ 0x64086408u);
-    h[7] = as_h2((b8 & 0x00F000F0u) ^ 0x64806480u);
-}
-
 template <int MR, int R, int EPI, typename OutT, bool XLDS, int PF, int NWV>
 __global__ __launch_bounds__(64 * NWV) void gemv_int4_kernel(const GemvParams p) {
     constexpr int NTH = 64 * NWV;                        // threads per block
@@ -864,6 +848,11 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     if (M > 8)
         return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K,
                              residual);
+    if (M == 1) {  // large N: the row-pair kernel
+        const xinfer_fused_desc one = {Y, W, S, bias, N};
+        int prc = XINFER_OK;
+        if (!pair_linear(st, &one, 1, X, y_f32, K, residual, &prc)) return prc;
+    }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);
@@ -966,6 +955,10 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
             if (rc) return rc;
         }
         return XINFER_OK;
+    }
+    if (M == 1 && !norm_in_kernel) {  // large N: the row-pair kernel (it has no norm prologue)
+        int prc = XINFER_OK;
+        if (!pair_linear(st, live, nd, X, false, K, false, &prc)) return prc;
     }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);

@@ -1,0 +1,307 @@
+// M = 1 INT4-G128-SYM GEMV streaming weight rows in pairs (gfx950).
+//
+// Same contract as the decode GEMV (src/ops/linear.cpp:165-305, and the
+// fused descriptors of linear.cpp:351-498) for large decode projections: one
+// activation row, K a multiple of 1024 in 4096..6144, N even, at least 32768
+// rows in the launch.  Two adjacent weight rows are K contiguous bytes, i.e.
+// P = K / 1024 pieces of 1 KB: a wave reads a row pair as P fully coalesced
+// 1 KB loads (lane j takes bytes 16j..16j+15 of each piece).  Streaming whole
+// 1 KB pieces reads faster on MI355X than the GEMV's 512-byte row pieces (a
+// pure read of the north-star matrix: 14.2-14.6 us in pairs against
+// 15.8-17.0 us in the GEMV's pattern).
+//
+//   * lane j's 16 bytes of piece i are chunk c = 64 i + j of the pair: row
+//     c / (K/32) of the pair, k = 32 (c % (K/32)).  That position is the
+//     same for every pair, so each lane keeps the activations of its P
+//     chunks in registers (permuted to the decode's pair order, with the
+//     chunk's bias term), loaded once: no LDS staging, no barrier.
+//   * decode and arithmetic as the GEMV: one v_bitop3_b32 per nibble pair
+//     gives exact biased fp16 integers, v_dot2_f32_f16 into ta / tb, the
+//     chunk's dot product is ta + tb/16 with ta started at the bias term,
+//     scaled by the fp16 group scale in FP32;
+//   * a wave owns a contiguous range of pairs (over all descriptors), so a
+//     row's sum never leaves its wave: 64-lane reduction per pair into a
+//     small per-wave LDS buffer; the results are stored after the loop.  No
+//     global store or load sits inside the streaming loop: on gfx9 the
+//     vector-memory counter counts both, and one there made the compiler
+//     drain the prefetch ring on every item (measured);
+//   * every load is a buffer load with a constant per-lane offset and a
+//     wave-uniform pair offset; one item (the P pieces of one pair) in flight
+//     while the previous one is computed.  The ring runs whole passes; the
+//     last item is computed after it, so no wave waits on a load issued past
+//     its end.
+
+#include "common.h"
+
+namespace xhip {
+
+struct PairDesc {
+    const uint8_t* W;   // [N][K/2]
+    const uint16_t* S;  // [N][K/128]
+    const float* bias;  // optional [N]
+    void* Y;            // [N] fp16 / fp32
+    int32_t N;          // even
+    int32_t pair_begin; // first pair of this descriptor in the pair space
+    int32_t residual;   // fp16 Y: Y = fp16(Y + fp16(result))
+};
+
+struct PairParams {
+    PairDesc d[4];
+    int32_t ndesc;
+    int32_t npairs;     // pairs over all descriptors
+    const f16* X;       // [K]
+};
+
+constexpr int kPairMaxPerWave = 128;  // pairs per wave (LDS results: 1 KB per wave)
+constexpr int kPairPF = 1;            // items in flight while one is computed
+
+template <int P, typename OutT>
+__global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p) {
+    constexpr int PF = kPairPF;
+    constexpr int K = 1024 * P;
+    constexpr int CPR = K / 32;       // 16-byte chunks per row
+    constexpr int NG = K / 128;       // scale groups per row
+    constexpr uint32_t kRowBytes = K / 2;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool hi = lane >= 32;
+
+    // this wave's pairs
+    const int64_t nwaves = (int64_t)gridDim.x * 4;
+    const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
+    const int q0 = (int)(gw * p.npairs / nwaves);
+    const int q1 = (int)((gw + 1) * p.npairs / nwaves);
+
+    // --- per-lane activations of the lane's P chunks (the same for every
+    // pair): raw loads first; they are permuted after the weight prefetch is
+    // issued (loads complete in order, so that waits for X alone)
+    u32x4 xr[P][4];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int c = 64 * i + lane;
+        const int cr = c < CPR ? c : c - CPR;
+        const u32x4* src = reinterpret_cast<const u32x4*>(p.X + cr * 32);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xr[i][v] = src[v];
+    }
+    f16x2 xp[P][16];  // the chunks' activations in the decode's pair order
+    float cb[P];      // chunk bias terms -(1032 sum x_even + 72 sum x_odd)
+
+    // per-lane byte offsets of the scales of piece i (within a pair's scales)
+    uint32_t soff[P];
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int c = 64 * i + lane;
+        const int row = c < CPR ? 0 : 1;
+        const int cr = c - row * CPR;
+        soff[i] = (uint32_t)(row * NG + (cr >> 2)) * 2u;
+    }
+
+    // --- items (pairs).  The descriptors' fields are read once and selected
+    // by wave-uniform compares (no kernel-argument load per item).
+    const int nd = p.ndesc;
+    const int pb1 = nd > 1 ? p.d[1].pair_begin : 0x7FFFFFFF;
+    const int pb2 = nd > 2 ? p.d[2].pair_begin : 0x7FFFFFFF;
+    const int pb3 = nd > 3 ? p.d[3].pair_begin : 0x7FFFFFFF;
+    const uint8_t* const dw[4] = {p.d[0].W, p.d[1].W, p.d[2].W, p.d[3].W};
+    const uint16_t* const ds[4] = {p.d[0].S, p.d[1].S, p.d[2].S, p.d[3].S};
+    const int pbs[4] = {0, pb1, pb2, pb3};
+    auto pick = [](int di, auto const (&a)[4]) { return di == 0 ? a[0] : di == 1 ? a[1] : di == 2 ? a[2] : a[3]; };
+    struct Item {
+        u32x4 w[P];
+        uint32_t s[P];
+    };
+    const int nitems = q1 - q0;
+    // a wave without pairs issues its prefetch against empty resources
+    const int live = nitems > 0 ? 1 : 0;
+    int lit = 0;  // load cursor (item index within the wave)
+    auto load_next = [&](Item& b) {
+        const int it = lit < nitems ? lit : (nitems > 0 ? nitems - 1 : 0);  // past the end: repeat
+        ++lit;
+        const int q = live ? q0 + it : 0;
+        const int di = (q >= pb1) + (q >= pb2) + (q >= pb3);
+        const int qq = q - pick(di, pbs);  // pair within the descriptor
+        const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(pick(di, dw) + (size_t)qq * 2 * kRowBytes), (short)0, (int)(2 * kRowBytes) * live, 0x00020000);
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void*)(pick(di, ds) + (size_t)qq * 2 * NG), (short)0, (int)(2 * NG * 2) * live, 0x00020000);
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(i * 1024 + lane * 16), 0, 2);
+            b.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff[i], 0, 0);
+        }
+    };
+
+    // --- per pair: the two rows' sums
+    float acc[2] = {0.0f, 0.0f};
+    auto compute_item = [&](const Item& b) {
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            f16x2 h[16];
+            decode16_biased(b.w[i].x, b.w[i].y, &h[0]);
+            decode16_biased(b.w[i].z, b.w[i].w, &h[8]);
+            float ta = cb[i], tb = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 16; k += 2) {
+                ta = dot2(h[k], xp[i][k], ta);
+                tb = dot2(h[k + 1], xp[i][k + 1], tb);
+            }
+            const float v = __builtin_fmaf(tb, 0.0625f, ta) * h2f((uint16_t)b.s[i]);
+            // piece i lies in row 0, row 1, or (P odd, i = P/2) splits at lane 32
+            if (64 * i + 63 < CPR) {
+                acc[0] += v;
+            } else if (64 * i >= CPR) {
+                acc[1] += v;
+            } else {
+                acc[0] += hi ? 0.0f : v;
+                acc[1] += hi ? v : 0.0f;
+            }
+        }
+    };
+
+    // the pair's two row sums into this wave's LDS buffer
+    __shared__ float res[4][2 * kPairMaxPerWave];
+    auto finish_pair = [&](int q) {
+        float r[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+            const float v = sum32(acc[rr]);
+            r[rr] = v + __shfl_xor(v, 32);
+            acc[rr] = 0.0f;
+        }
+        if (lane < 2) res[wave][2 * (q - q0) + lane] = lane ? r[1] : r[0];
+    };
+
+    Item buf[PF + 1];
+#pragma unroll
+    for (int j = 0; j < PF; ++j) load_next(buf[j]);
+    __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        float se = 0.0f, so = 0.0f;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t xa[4] = {xr[i][v].x, xr[i][v].y, xr[i][v].z, xr[i][v].w};
+            permute_x8(xa, &xp[i][4 * v]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const f16x2 x2 = as_h2(xa[j]);
+                se += (float)x2.x;
+                so += (float)x2.y;
+            }
+        }
+        cb[i] = -(1032.0f * se + 72.0f * so);
+    }
+
+    // The ring's body has no branch around a load and no global memory
+    // access besides the weight loads (exact vmcnt bookkeeping).  It runs
+    // whole passes; the loads it issues past the wave's end are never
+    // waited on, and the last items (already in registers) follow it.
+    int cit = 0;  // compute cursor
+    int base = 0;
+    for (; base + PF + 1 <= nitems; base += PF + 1) {
+#pragma unroll
+        for (int j = 0; j <= PF; ++j) {
+            load_next(buf[(j + PF) % (PF + 1)]);
+            __builtin_amdgcn_sched_barrier(0);  // the next item's loads go out before this compute
+            compute_item(buf[j]);
+            finish_pair(q0 + cit++);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PF; ++j) {
+        if (base + j < nitems) {
+            compute_item(buf[j]);
+            finish_pair(q0 + cit++);
+        }
+    }
+
+    // results of this wave's rows, per descriptor (wave-uniform), one lane
+    // per row: contiguous stores
+    for (int di = 0; di < p.ndesc; ++di) {
+        const PairDesc& d = p.d[di];
+        const int qb = q0 > d.pair_begin ? q0 : d.pair_begin;
+        const int qe = q1 < d.pair_begin + d.N / 2 ? q1 : d.pair_begin + d.N / 2;
+        for (int i = 2 * (qb - q0) + lane; i < 2 * (qe - q0); i += 64) {
+            const int n = 2 * (q0 - d.pair_begin) + i;
+            float v = res[wave][i];
+            if (d.bias) v += d.bias[n];
+            OutT* y = reinterpret_cast<OutT*>(d.Y) + n;
+            if (d.residual)  // add_inplace after the projection (elementwise.cpp:227)
+                *y = (OutT)((float)*y + (float)(OutT)v);
+            else
+                *y = (OutT)v;
+        }
+    }
+}
+
+}  // namespace xhip
+
+using namespace xhip;
+
+namespace xhip_host {
+
+namespace {
+
+typedef void (*PairKernel)(PairParams);
+
+template <typename OutT>
+PairKernel pair_kernel_for(int P) {
+    switch (P) {
+        case 4: return gemv_pair_int4_kernel<4, OutT>;
+        case 5: return gemv_pair_int4_kernel<5, OutT>;
+        case 6: return gemv_pair_int4_kernel<6, OutT>;
+        default: return nullptr;
+    }
+}
+
+}  // namespace
+
+// Whether the pair kernel takes an M = 1 launch of n_total rows: K a
+// multiple of 1024 in 4096..6144 and at least 32768 rows.  Measured against
+// the GEMV on MI355X (graph-replayed, K = 4096 / 5120 / 6144): N = 34816
+// 14.4 / 16.9 / 19.8 us -> 13.9 / 16.3 / 19.6 us; below 32768 rows neither
+// wins consistently (N = 8192 and 17408 at K = 5120 are 1-6 % faster on the
+// GEMV).
+bool pair_takes(int64_t M, int64_t K, int64_t n_total) {
+    return M == 1 && K % 1024 == 0 && K >= 4096 && K <= 6144 && n_total >= 32768;
+}
+
+// Returns 1 when the launch is left to the GEMV (odd N, shape not taken),
+// else 0 with *rc the launch status.  One 4-wave block per CU (two per CU
+// measured 8-10 % slower), more when a wave would exceed kPairMaxPerWave
+// pairs.
+int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
+                int64_t K, bool residual, int* rc) {
+    if (nd < 1 || nd > 4) return 1;
+    int64_t rows = 0;
+    for (int i = 0; i < nd; ++i) {
+        if (descs[i].N % 2) return 1;
+        rows += descs[i].N;
+    }
+    if (!pair_takes(1, K, rows)) return 1;
+    PairParams p = {};
+    int pairs = 0;
+    for (int i = 0; i < nd; ++i) {
+        p.d[i] = PairDesc{descs[i].W_int4, reinterpret_cast<const uint16_t*>(descs[i].scales), descs[i].bias,
+                          descs[i].Y, (int32_t)descs[i].N, pairs, residual ? 1 : 0};
+        pairs += (int)(descs[i].N / 2);
+    }
+    p.ndesc = nd;
+    p.npairs = pairs;
+    p.X = reinterpret_cast<const f16*>(X);
+    PairKernel k = y_f32 ? pair_kernel_for<float>((int)(K / 1024)) : pair_kernel_for<f16>((int)(K / 1024));
+    if (!k) return 1;
+    int64_t blocks = num_cus();
+    const int64_t need = (p.npairs + 4LL * kPairMaxPerWave - 1) / (4LL * kPairMaxPerWave);
+    if (blocks < need) blocks = need;
+    if (blocks > 65535) return 1;
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    *rc = launch_status();
+    return 0;
+}
+
+}  // namespace xhip_host
