@@ -211,7 +211,10 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // the first round (up to kStageUnroll chunks per thread) are issued
     // before the weight prefetch: loads complete in issue order, so the
     // staging then waits for X alone while the weight items stay in flight.
-    constexpr int kStageUnroll = 4;
+    // A later round would wait behind the prefetch: 4-wave blocks (one per
+    // SIMD, registers to spare) take 8 chunks per thread, so an X slice of up
+    // to 128 KB is one round (K = 17408, M = 8: 92 KB, 5.75 chunks a thread).
+    constexpr int kStageUnroll = NW == 4 ? 8 : 4;
     const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
     auto get = [&](int i, u32x4 (&xv)[4]) {
         const int m = i % M;
