@@ -36,6 +36,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+#include <cstdint>
 #include <mutex>
 
 #include "common.h"
@@ -55,6 +57,7 @@ struct MbDesc {
     int32_t block_begin; // first block of this descriptor
     int32_t range_begin; // first tile range of this descriptor (counters, parts)
     int32_t residual;    // MB_PLAIN, fp16 Y: Y = fp16(Y + fp16(result))
+    int32_t nr;          // tile ranges of this descriptor (its tiles split evenly over them)
 };
 
 struct MbParams {
@@ -70,7 +73,7 @@ struct MbParams {
     int32_t K;
     int32_t ks;          // k-slices per tile range
     int32_t gps;         // groups per k-slice (the last slice may be shorter)
-    int32_t tiles_blk;   // 16-row tiles per block
+    int32_t tiles_blk;   // 16-row tiles of the largest range
     int32_t nranges;     // tile ranges over all descriptors
     int32_t lkw;         // log2 of the waves that share a run of tiles, splitting its groups
 };
@@ -134,8 +137,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     const int range = local / ks;
     const int slice = local - range * ks;
     const int grange = d.range_begin + range;
-    const int n0 = range * p.tiles_blk * 16;
-    const int rows_here = min(p.tiles_blk * 16, N - n0);
+    // tiles split evenly over the descriptor's ranges (counts differ by at most one)
+    const int ntiles = (N + 15) >> 4;
+    const int tb = range * ntiles / d.nr, te = (range + 1) * ntiles / d.nr;
+    const int n0 = tb * 16;
+    const int rows_here = min(te * 16, N) - n0;
     const int tiles_here = (rows_here + 15) >> 4;
     const int ng = K >> 7;
     const int g0 = slice * p.gps;
@@ -488,15 +494,19 @@ int env_int(const char* name, int dflt) {
 }
 
 struct MbOverrides {
-    int nw, ks, bpc, min_m, raise, kw;
+    int nw, ks, bpc, min_m, raise, kw, balance;
 };
 const MbOverrides& mb_overrides() {
     static const MbOverrides o = {env_int("XINFER_MB_NW", 0),
                                   env_int("XINFER_MB_KS", 0), env_int("XINFER_MB_BPC", 0),
                                   env_int("XINFER_MB_MIN_M", 0), env_int("XINFER_MB_RAISE", -1),
-                                  env_int("XINFER_MB_KW", 0)};
+                                  env_int("XINFER_MB_KW", 0), env_int("XINFER_MB_BALANCE", 1)};
     return o;
 }
+
+// Prologue of a wave (X staging share, ring fill, epilogue) in units of one
+// group of one tile, for the planner's cost model.
+constexpr int64_t kMbWaveSetup = 8;
 
 constexpr size_t kMaxLds = 160 * 1024;
 // Chunked-prefill rows 9..16 fill the 16-row MFMA tile (N = 17408,
@@ -630,6 +640,68 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
         for (int i = 0; i < p.ndesc; ++i) ranges += ((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk;
         if (ov.kw > 0 || kw >= kw_cap || ranges * ks * 2 >= cus) break;
     }
+    // Ranges per descriptor: ceil(tiles / tiles_blk), tiles split evenly.
+    int nrd[4] = {1, 1, 1, 1};
+    for (int i = 0; i < p.ndesc; ++i) nrd[i] = (int)(((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk);
+    // Balance.  A wave's time is its tiles times its groups, and a CU's waves
+    // share its SIMDs, so a launch takes about (blocks per CU) x (tiles per
+    // wave) x (groups per wave) units plus a prologue per wave.  The plan
+    // above rounds tiles per block up and may leave CUs with two blocks
+    // while others have one (gate/up SwiGLU, M = 4: 272 blocks of 4 tiles on
+    // 256 CUs).  Candidates with exactly c blocks per CU (c <= bpc), tiles
+    // spread over the ranges in proportion, and kw waves per tile (every run
+    // of waves with a tile) are scored the same way; the lowest wins, the
+    // plan above on ties.
+    auto cost = [&](int64_t nblocks, int64_t tmax, int kwc) {
+        const int64_t per_cu = (nblocks + cus - 1) / cus;
+        const int64_t runs = nw / kwc;
+        return per_cu * (((tmax + runs - 1) / runs) * ((gps + kwc - 1) / kwc) + kMbWaveSetup);
+    };
+    if (ov.balance && ov.kw <= 0) {
+        int64_t best = cost(ranges * ks, tiles_blk, kw);
+        for (int c = 1; c <= bpc; ++c) {
+            int64_t R = (int64_t)cus * c / ks;
+            if (R > tiles_total) R = tiles_total;
+            if (R < p.ndesc) continue;
+            int nr[4] = {1, 1, 1, 1};
+            int64_t used = 0;
+            for (int i = 0; i < p.ndesc; ++i) {
+                const int64_t t = (p.d[i].N + 15) / 16;
+                nr[i] = (int)std::max<int64_t>(1, std::min<int64_t>(t, t * R / tiles_total));
+                used += nr[i];
+            }
+            while (used < R) {  // leftover ranges to the descriptor with the most tiles per range
+                int bi = -1;
+                int64_t bt = 0;
+                for (int i = 0; i < p.ndesc; ++i) {
+                    const int64_t t = (p.d[i].N + 15) / 16;
+                    if (nr[i] < t && (t + nr[i] - 1) / nr[i] > bt) { bt = (t + nr[i] - 1) / nr[i]; bi = i; }
+                }
+                if (bi < 0) break;
+                ++nr[bi];
+                ++used;
+            }
+            int64_t tmax = 0, tmin = INT64_MAX;
+            for (int i = 0; i < p.ndesc; ++i) {
+                const int64_t t = (p.d[i].N + 15) / 16;
+                tmax = std::max<int64_t>(tmax, (t + nr[i] - 1) / nr[i]);
+                tmin = std::min<int64_t>(tmin, t / nr[i]);
+            }
+            for (int kwc = 1; kwc <= kw_cap; kwc *= 2) {
+                if (tmin < nw / kwc) continue;  // a run of waves without a tile
+                const size_t l = (size_t)gps * xg + (size_t)tmax * 16 * M * E * 4 * kwc + 2 * nw * 4 + 16;
+                if (l * c > kMaxLds) continue;
+                const int64_t cc = cost(used * ks, tmax, kwc);
+                if (cc < best) {
+                    best = cc;
+                    kw = kwc;
+                    tiles_blk = tmax;
+                    ranges = used;
+                    for (int i = 0; i < 4; ++i) nrd[i] = nr[i];
+                }
+            }
+        }
+    }
     int lkw = 0;
     while ((1 << lkw) < kw) ++lkw;
     const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16;
@@ -649,7 +721,8 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     int blocks = 0, rbeg = 0;
     int64_t wsoff = 0;
     for (int i = 0; i < p.ndesc; ++i) {
-        const int r = (int)(((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk);
+        const int r = nrd[i];
+        p.d[i].nr = r;
         p.d[i].block_begin = blocks;
         p.d[i].range_begin = rbeg;
         p.ws_desc[i] = wsoff;
