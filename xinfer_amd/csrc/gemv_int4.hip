@@ -70,8 +70,8 @@ struct GemvParams {
 // dynamic LDS in front of the X pieces: RMSNorm partial sums (8 per wave,
 // up to 8 waves) and the row factors (8), padded to keep the pieces 16-byte
 // aligned
-constexpr int kGemvLdsHead = 512;
-static_assert((8 * 8 + 8) * 4 <= kGemvLdsHead, "RMSNorm scratch for up to 8 waves");
+constexpr int kGemvLdsHead = 1024;
+static_assert((16 * 8 + 8) * 4 <= kGemvLdsHead, "RMSNorm scratch for up to 16 waves");
 
 template <int RR>
 struct ItemRegs {
@@ -511,6 +511,7 @@ namespace {
 
 struct GemvPlan {
     int mr, r, pf, blocks, nw;
+    bool w16;  // M = 1, R = 2: one 16-wave block per CU in place of two 8-wave blocks
     bool xlds;
     size_t lds;
 };
@@ -518,49 +519,53 @@ struct GemvPlan {
 typedef void (*GemvKernel)(GemvParams);
 
 template <int MR, int R, int EPI, typename OutT, int PF>
-GemvKernel pick_kernel(bool xlds) {
-    // M <= 2 with R = 2 runs 8-wave blocks (gemv_waves), everything else 4
+GemvKernel pick_kernel(bool xlds, bool w16) {
+    // M <= 2 with R = 2 runs 8-wave blocks (gemv_waves), everything else 4;
+    // M = 1 with R = 2 and X in LDS may run 16-wave blocks
     constexpr int NWV = (MR <= 2 && R == 2) ? 8 : 4;
+    if constexpr (MR == 1 && R == 2 && PF == 1)
+        if (w16 && xlds) return gemv_int4_kernel<MR, R, EPI, OutT, true, PF, 16>;
     return xlds ? gemv_int4_kernel<MR, R, EPI, OutT, true, PF, NWV>
                 : gemv_int4_kernel<MR, R, EPI, OutT, false, PF, NWV>;
 }
 
 template <int MR, int R, int EPI, typename OutT>
-GemvKernel pick_pf(bool xlds, int pf) {
+GemvKernel pick_pf(bool xlds, int pf, bool w16) {
     if (MR == 1 && EPI != EPI_ARGMAX) {
-        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds);
-        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
-        return pick_kernel<MR, R, EPI, OutT, 3>(xlds);
+        if (pf <= 1) return pick_kernel<MR, R, EPI, OutT, 1>(xlds, w16);
+        if (pf == 2) return pick_kernel<MR, R, EPI, OutT, 2>(xlds, w16);
+        return pick_kernel<MR, R, EPI, OutT, 3>(xlds, w16);
     }
-    return pick_kernel<MR, R, EPI, OutT, 2>(xlds);
+    return pick_kernel<MR, R, EPI, OutT, 2>(xlds, w16);
 }
 
 template <int EPI, typename OutT>
-GemvKernel kernel_for(int mr, int r, bool xlds, int pf) {
+GemvKernel kernel_for(int mr, int r, bool xlds, int pf, bool w16 = false) {
     switch (mr) {
         case 1:
-            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf)
-                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf) : pick_pf<1, 4, EPI, OutT>(xlds, pf);
+            return r == 1 ? pick_pf<1, 1, EPI, OutT>(xlds, pf, false)
+                 : r == 2 ? pick_pf<1, 2, EPI, OutT>(xlds, pf, w16) : pick_pf<1, 4, EPI, OutT>(xlds, pf, false);
         case 2:
-            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf) : pick_pf<2, 4, EPI, OutT>(xlds, pf);
+            return r == 2 ? pick_pf<2, 2, EPI, OutT>(xlds, pf, false) : pick_pf<2, 4, EPI, OutT>(xlds, pf, false);
         case 4:
-            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf) : pick_pf<4, 2, EPI, OutT>(xlds, pf);
+            return r == 1 ? pick_pf<4, 1, EPI, OutT>(xlds, pf, false) : pick_pf<4, 2, EPI, OutT>(xlds, pf, false);
         default:
-            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf) : pick_pf<8, 2, EPI, OutT>(xlds, pf);
+            return r == 1 ? pick_pf<8, 1, EPI, OutT>(xlds, pf, false) : pick_pf<8, 2, EPI, OutT>(xlds, pf, false);
     }
 }
 
-// Tuning overrides (read once): XINFER_GEMV_R, XINFER_GEMV_PF, XINFER_GEMV_BPC.
+// Tuning overrides (read once): XINFER_GEMV_R, XINFER_GEMV_PF, XINFER_GEMV_BPC,
+// XINFER_GEMV_W16.
 int env_int(const char* name, int dflt) {
     const char* v = getenv(name);
     return (v && *v) ? atoi(v) : dflt;
 }
 struct Overrides {
-    int r, pf, bpc;
+    int r, pf, bpc, w16;
 };
 const Overrides& overrides() {
     static const Overrides o = {env_int("XINFER_GEMV_R", 0), env_int("XINFER_GEMV_PF", 0),
-                                env_int("XINFER_GEMV_BPC", 0)};
+                                env_int("XINFER_GEMV_BPC", 0), env_int("XINFER_GEMV_W16", -1)};
     return o;
 }
 
@@ -696,11 +701,22 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
         const size_t lds_cap = gemv_lds_cap(gemv_waves(mr, r), x_bytes);
         const bool xlds = x_bytes + 4096 <= lds_cap;
         const int pf = ov.pf > 0 ? ov.pf : (mr == 1 ? 1 : 2);
-        const int nw = gemv_waves(mr, r);
-        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf);
+        // Two 8-wave blocks per CU -> one 16-wave block (same waves per SIMD,
+        // X staged once per CU).  A CU's second 8-wave block gets its X
+        // after the first block's weight prefetch (a CU's loads return in
+        // order) and starts streaming ~5 us late.  Measured, graph-replayed:
+        // fused QKV 9.13 -> 8.95 us, LA in_proj 10.13 -> 10.02, decode layer
+        // M = 1 45.95 -> 45.4; single projections lose a little (config 1
+        // 16.97 -> 17.19, q-proj 5.63 -> 5.67, N = 48 3.53 -> 3.71), so the
+        // default is fused launches only (XINFER_GEMV_W16: 0 never, 1 always).
+        const bool w16_ok = ov.bpc <= 0 && EPI != EPI_ARGMAX && mr == 1 && r == 2 && pf == 1 && xlds &&
+                            !gemv_one_block_per_cu(gemv_waves(mr, r), x_bytes);
+        const bool w16 = w16_ok && (ov.w16 > 0 || (ov.w16 < 0 && p.ndesc >= 2));
+        const int nw = w16 ? 16 : gemv_waves(mr, r);
+        GemvKernel k = kernel_for<EPI, OutT>(mr, r, xlds, pf, w16);
         int64_t rows = 0;
         size_t lds = 0;
-        int bpc = ov.bpc > 0 ? ov.bpc : (xlds && gemv_one_block_per_cu(nw, x_bytes)) ? 1 : 2;
+        int bpc = ov.bpc > 0 ? ov.bpc : ((xlds && gemv_one_block_per_cu(nw, x_bytes)) || w16) ? 1 : 2;
         for (int pass = 0; pass < 3; ++pass) {
             const int64_t target = (int64_t)cus * bpc;
             rows = (total_rows + target - 1) / target;
@@ -742,6 +758,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
         best.r = r;
         best.pf = pf;
         best.nw = nw;
+        best.w16 = w16;
         best.xlds = xlds;
         best.lds = lds;
         rows_blk = (int32_t)rows;
@@ -761,7 +778,7 @@ GemvPlan plan_gemv(GemvParams& p, int mr) {
 
 template <int EPI, typename OutT>
 int launch_plan(const GemvParams& p, const GemvPlan& pl, hipStream_t st) {
-    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf);
+    GemvKernel k = kernel_for<EPI, OutT>(pl.mr, pl.r, pl.xlds, pl.pf, pl.w16);
     if (!allow_lds(k, pl.lds)) return XINFER_ERR_HIP;
     hipLaunchKernelGGL(k, dim3(pl.blocks), dim3(64 * pl.nw), pl.lds, st, p);
     return XINFER_OK;
