@@ -596,13 +596,20 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     // slices leave one block per CU and lose (gate/up M = 8 42.1 -> 45.7 us).
     const bool long_k8 = EPI != MB_ARGMAX && mr == 8 && (size_t)ng * xg > 4 * 48 * 1024;
     if (long_k8) x_budget = 96 * 1024;
+    // All of X within 80 KB at the 8-row stride (K <= 5120): one slice, no
+    // split-K combine, 4 waves at one block per CU (with the balanced plan
+    // below).  Measured at M = 8: gate/up SwiGLU 37.1 -> 29.5 us, fused QKV
+    // 15.9 -> 13.3 us; o_proj (K = 6144, 96 KB) lost (11.1 -> 11.6), so the
+    // limit stays at 80 KB.
+    const bool whole8 = EPI != MB_ARGMAX && mr == 8 && (size_t)ng * xg <= 80 * 1024;
+    if (whole8) x_budget = 80 * 1024;
     int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
     if (EPI == MB_ARGMAX) ks = 1;
     if (ks > ng) ks = ng;
     const size_t slice = (size_t)ng * xg / ks;
     // X slice beyond nw_at: 8 waves.  The LM head keeps 4 waves at one block
     // per CU (M = 8, N = 151936: 94.0 -> 89.5 us against 8 waves).
-    const size_t nw_at = long_k8 ? 96 * 1024 : 64 * 1024;
+    const size_t nw_at = (long_k8 || whole8) ? 96 * 1024 : 64 * 1024;
     int nw = ov.nw > 0 ? ov.nw : (EPI != MB_ARGMAX && slice > nw_at) ? 8 : 4;
     nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
     int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
