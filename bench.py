@@ -368,7 +368,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         lnw = [torch.linspace(0.5, 1.5, H, dtype=torch.float32, device=dev) for _ in range(2)]
         nbytes = sum(gemv_bytes(1, r.W[0].shape[0], r.W[0].shape[1] * 2, 0, 0)
                      for r in layers[0].values())
-        for M in (1, 4):
+        for M in (1, 4, 8):  # decode, and the speculative verify rows (forward.cpp:729-732)
             f16 = dict(dtype=torch.float16, device=dev)
             resid = torch.from_numpy(synth.activations(0, M, H)).view(torch.float16).to(dev)
             bq, bk, bv = (torch.empty((M, n), **f16) for n in (Q, KV, KV))
