@@ -603,6 +603,13 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     // limit stays at 80 KB.
     const bool whole8 = EPI != MB_ARGMAX && mr == 8 && (size_t)ng * xg <= 80 * 1024;
     if (whole8) x_budget = 80 * 1024;
+    // 9-16 rows (16-row stride) with X within two 80 KB slices (K <= 5120):
+    // two slices and 8-wave blocks instead of three 53 KB slices of 4 waves.
+    // Measured at N = 17408, K = 5120, M = 9 / 12 / 16: linear 22.3 / 24.4 /
+    // 27.4 -> 20.0 / 21.2 / 22.5 us, SwiGLU 40.9 / 44.4 / 49.3 -> 38.3 /
+    // 40.4 / 42.8 us.
+    const bool two16 = EPI != MB_ARGMAX && mr == 16 && (size_t)ng * xg <= 160 * 1024;
+    if (two16) x_budget = 80 * 1024;
     int ks = ov.ks > 0 ? ov.ks : (int)((ng * xg + x_budget - 1) / x_budget);
     if (EPI == MB_ARGMAX) ks = 1;
     if (ks > ng) ks = ng;
