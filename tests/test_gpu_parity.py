@@ -448,3 +448,46 @@ def test_prefill_fused_descs_m64():
     ops.linear_int4_fused(f16_dev(Xb), descs, 3, M, K)
     for Y, ref in zip(outs, refs):
         check_f16_tol(to_np(Y), ref)
+
+
+# Decode-shape plans of the small-batch planner and the GEMV planner: gate/up
+# SwiGLU at M = 4 (256 blocks, four waves per tile) and M = 8 (one 80 KB X
+# slice), fused QKV at M = 2 (GEMV, one block per CU) and M = 8 (one slice),
+# and a 12-row chunk (two 80 KB slices, 8-wave blocks), all at K = 5120.
+@pytest.mark.parametrize("M", [4, 8])
+def test_planned_swiglu_decode_shape(M):
+    import torch
+    ops = _ops()
+    N, K = 17408, 5120
+    W = synth.packed_weights(50 + M, 2 * N, K)
+    S = synth.scales(50 + M, 2 * N, K, 0.01)
+    Xb = synth.activations(50 + M, M, K)
+    dW, dS = to_dev(W), f16_dev(S)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), dW[:N], dS[:N], dW[N:], dS[N:], M, N, K)
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb), W[:N], S[:N], W[N:], S[N:], M, N, K,
+                             nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y), ref))
+
+
+@pytest.mark.parametrize("M", [2, 8])
+def test_planned_fused_qkv_decode_shape(M):
+    import torch
+    ops = _ops()
+    K = 5120
+    Xb = synth.activations(60 + M, M, K)
+    X = oracle.f16_to_f32(Xb)
+    descs, outs, refs = [], [], []
+    for p, Np in enumerate((12288, 1024, 1024)):
+        W, S = synth.packed_weights(61 + p, Np, K), synth.scales(61 + p, Np, K)
+        refs.append(oracle.linear_int4(X, W, S, M, Np, K, nthreads=cpu_threads()))
+        Y = _empty((M, Np), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, Np))
+    ops.linear_int4_fused(f16_dev(Xb), descs, 3, M, K)
+    for Y, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Y), ref))
+
+
+def test_planned_chunk_rows_m12():
+    print(_linear_case(12, 17408, 5120, seed=12, sigma=0.01))
