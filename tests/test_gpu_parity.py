@@ -453,6 +453,7 @@ def test_prefill_fused_descs_m64():
 # Decode-shape plans of the small-batch planner and the GEMV planner: gate/up
 # SwiGLU at M = 4 (256 blocks, four waves per tile) and M = 8 (one 80 KB X
 # slice), fused QKV at M = 2 (GEMV, one block per CU) and M = 8 (one slice),
+# the linear-attention in_proj at M = 4 / 8,
 # and a 12-row chunk (two 80 KB slices, 8-wave blocks), all at K = 5120.
 @pytest.mark.parametrize("M", [4, 8])
 def test_planned_swiglu_decode_shape(M):
@@ -470,21 +471,24 @@ def test_planned_swiglu_decode_shape(M):
     print(check_f16_tol(to_np(Y), ref))
 
 
-@pytest.mark.parametrize("M", [2, 8])
-def test_planned_fused_qkv_decode_shape(M):
+# (the linear-attention in_proj's two 48-row descriptors get at least one
+# range each from the balanced plan)
+@pytest.mark.parametrize("M,Ns", [(2, (12288, 1024, 1024)), (8, (12288, 1024, 1024)),
+                                  (4, (10240, 6144, 48, 48)), (8, (10240, 6144, 48, 48))])
+def test_planned_fused_decode_shape(M, Ns):
     import torch
     ops = _ops()
     K = 5120
     Xb = synth.activations(60 + M, M, K)
     X = oracle.f16_to_f32(Xb)
     descs, outs, refs = [], [], []
-    for p, Np in enumerate((12288, 1024, 1024)):
+    for p, Np in enumerate(Ns):
         W, S = synth.packed_weights(61 + p, Np, K), synth.scales(61 + p, Np, K)
         refs.append(oracle.linear_int4(X, W, S, M, Np, K, nthreads=cpu_threads()))
         Y = _empty((M, Np), torch.float16)
         outs.append(Y)
         descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, Np))
-    ops.linear_int4_fused(f16_dev(Xb), descs, 3, M, K)
+    ops.linear_int4_fused(f16_dev(Xb), descs, len(Ns), M, K)
     for Y, ref in zip(outs, refs):
         print(check_f16_tol(to_np(Y), ref))
 
