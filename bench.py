@@ -324,11 +324,12 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         for M in (1, 4):
             X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
             Xn = torch.empty_like(X)
+            ws = torch.empty(max(1, M * K * 2), dtype=torch.uint8, device=dev)
             Ys = [torch.empty((M, N), dtype=torch.float16, device=dev) for N in Ns]
 
-            def fused(i, rigs=rigs, Ys=Ys, X=X, M=M):
+            def fused(i, rigs=rigs, Ys=Ys, X=X, M=M, ws=ws):
                 ds = [ops.FusedProjectionDesc(Y, r.W[i], r.S[i], None, N) for Y, r, N in zip(Ys, rigs, Ns)]
-                ops.rmsnorm_linear_int4_fused(X, nw, 1e-6, ds, 3, M, K)
+                ops.rmsnorm_linear_int4_fused(X, nw, 1e-6, ds, 3, M, K, workspace=ws)
 
             def separate(i, rigs=rigs, Ys=Ys, X=X, Xn=Xn, M=M):
                 ops.rmsnorm(Xn, X, nw, M, K, 1e-6)
@@ -374,15 +375,16 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
             bq, bk, bv = (torch.empty((M, n), **f16) for n in (Q, KV, KV))
             attn = torch.from_numpy(synth.activations(1, M, AO)).view(torch.float16).to(dev)
             act = torch.empty((M, I), **f16)
+            ws = torch.empty(M * H * 2, dtype=torch.uint8, device=dev)  # normalised rows (M >= 2)
 
-            def layer_step(i, M=M, resid=resid, bq=bq, bk=bk, bv=bv, attn=attn, act=act):
+            def layer_step(i, M=M, resid=resid, bq=bq, bk=bk, bv=bv, attn=attn, act=act, ws=ws):
                 Lr = layers[i % 2]
                 ds = [ops.FusedProjectionDesc(Y, Lr[n].W[0], Lr[n].S[0], None, N)
                       for Y, n, N in ((bq, "q", Q), (bk, "k", KV), (bv, "v", KV))]
-                ops.rmsnorm_linear_int4_fused(resid, lnw[0], 1e-6, ds, 3, M, H)
+                ops.rmsnorm_linear_int4_fused(resid, lnw[0], 1e-6, ds, 3, M, H, workspace=ws)
                 ops.linear_int4_residual(resid, attn, Lr["o"].W[0], Lr["o"].S[0], None, M, H, AO)
                 ops.rmsnorm_mlp_gate_up_swiglu_int4(act, resid, lnw[1], 1e-6, Lr["g"].W[0], Lr["g"].S[0],
-                                                    Lr["u"].W[0], Lr["u"].S[0], M, I, H)
+                                                    Lr["u"].W[0], Lr["u"].S[0], M, I, H, workspace=ws)
                 ops.linear_int4_residual(resid, act, Lr["d"].W[0], Lr["d"].S[0], None, M, H, I)
             _, eg = time_launches(torch, layer_step, 256, warm, 2, graph=True)
             _, ee = time_launches(torch, layer_step, 256, warm, 2, graph=False)

@@ -23,11 +23,22 @@
  * aligned (XINFER_ERR_MISALIGNED). As in the reference (src/ops/linear.cpp:176,
  * 359, 513) M, N or K <= 0 is a no-op that returns XINFER_OK.
  *
- * No entry point allocates device memory, except xinfer_argmax_f32 and
- * xinfer_lm_head_argmax_int4 when called with scratch == NULL (they then use
- * a library-owned per-device buffer, as the reference's argmax falls back to
- * its own allocation, src/ops/sampling.cpp:28-31).  Kernels never synchronise
- * the host, so calls can be captured into a hipGraph when scratch is given.
+ * No projection entry point allocates device memory or synchronises: the
+ * first call of any shape can be captured into a hipGraph.  The small-batch
+ * kernel's cross-block split-K partials live in a static device array that
+ * the code object loader places with the library's kernels (32 slots per
+ * device, one owned by each stream that calls; with more streams than slots
+ * a call plans without the cross-block split).  Calls on different streams
+ * may therefore overlap.  A graph holds the slot of the stream it was
+ * captured on: replays of graphs captured on one stream must not overlap
+ * each other or that stream's work.  The only allocating calls are
+ * xinfer_argmax_f32 and xinfer_lm_head_argmax_int4 given scratch == NULL
+ * (a library-owned buffer per device and stream, grown on demand, as the
+ * reference's argmax falls back to its own allocation,
+ * src/ops/sampling.cpp:28-31); pass scratch to keep them capturable.
+ * The RMSNorm + projection entry points take a caller-owned workspace for
+ * the normalised rows (the reference's forward_layer writes them to an
+ * arena buffer, src/targets/qwen3_8/forward.cpp:112-125).
  */
 #ifndef XINFER_HIP_XINFER_OPS_H
 #define XINFER_HIP_XINFER_OPS_H
@@ -211,29 +222,36 @@ int xinfer_rmsnorm_f16(void* stream, void* out, const void* in, const float* wei
  * a = fp16(fp32(a) + fp32(b)). */
 int xinfer_add_inplace_f16(void* stream, void* a, const void* b, int64_t num_elements);
 
+/* Bytes of workspace the two RMSNorm + projection entry points below need
+ * for M rows of K: 0 when the norm runs inside the projection kernel (M = 1,
+ * K up to ~6k), else M * K * 2 (the normalised fp16 rows). */
+size_t xinfer_rmsnorm_projection_workspace_bytes(int64_t M, int64_t K);
+
 /* rmsnorm (rmsnorm.h:17-23) fused with linear_int4_fused (linear.h:97-103):
  * the input-norm + QKV / linear-attention in_proj pair of forward.cpp:112-125
  * and :237-247.  The projections see exactly the fp16 normalised X that
  * xinfer_rmsnorm_f16 would write (up to the order of the sum of squares).
  * Any M: at M = 1 the norm runs inside the projection kernel; otherwise the
- * normalised rows go through a per-device library buffer (allocated on the
- * first call of a size, so capture a graph after a warm-up call; calls on
- * different streams of one device must not overlap). */
+ * normalised rows go to `workspace` (16-byte aligned, at least
+ * xinfer_rmsnorm_projection_workspace_bytes(M, K) bytes, else
+ * XINFER_ERR_SCRATCH; NULL is fine when that is 0). */
 int xinfer_rmsnorm_linear_int4_fused_f16(void* stream, const void* X,
                                          const float* norm_weight, float eps,
                                          const xinfer_fused_desc* descs,
                                          int32_t num_descs, int64_t M, int64_t K,
-                                         int32_t group_size);
+                                         int32_t group_size, void* workspace,
+                                         size_t workspace_bytes);
 
 /* rmsnorm fused with mlp_gate_up_swiglu_int4 (linear.h:117-127): the
- * post-attention norm + gate/up pair of forward.cpp:273-281.  Any M, as
- * xinfer_rmsnorm_linear_int4_fused_f16. */
+ * post-attention norm + gate/up pair of forward.cpp:273-281.  Any M; the
+ * workspace as xinfer_rmsnorm_linear_int4_fused_f16. */
 int xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
                                                const float* norm_weight, float eps,
                                                const uint8_t* W_gate, const void* scales_gate,
                                                const uint8_t* W_up, const void* scales_up,
                                                int64_t M, int64_t N, int64_t K,
-                                               int32_t group_size);
+                                               int32_t group_size, void* workspace,
+                                               size_t workspace_bytes);
 
 /* linear_int4 (linear.h:30-39) fused with add_inplace (elementwise.h:22):
  * residual[m][n] = fp16(residual + fp16(linear(X) + bias)), bit-identical to

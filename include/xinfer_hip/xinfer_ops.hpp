@@ -163,26 +163,34 @@ inline void add_inplace(hipStream_t s, half* a, const half* b, int64_t num_eleme
     detail::check("add_inplace", xinfer_add_inplace_f16(detail::q(s), a, b, num_elements));
 }
 
-// rmsnorm + linear_int4_fused in one call (forward.cpp:112-125, 237-247)
+// Workspace bytes of the two rmsnorm + projection calls below (0 at M = 1).
+inline size_t rmsnorm_projection_workspace_size(int64_t M, int64_t K) {
+    return xinfer_rmsnorm_projection_workspace_bytes(M, K);
+}
+
+// rmsnorm + linear_int4_fused in one call (forward.cpp:112-125, 237-247);
+// workspace: caller-owned, rmsnorm_projection_workspace_size(M, K) bytes
 inline void rmsnorm_linear_int4_fused(hipStream_t s, const half* X, const float* norm_weight, float eps,
                                       const FusedProjectionDesc* descs, int num_descs, int64_t M,
-                                      int64_t K, int group_size = 128) {
+                                      int64_t K, int group_size = 128, void* workspace = nullptr,
+                                      size_t workspace_bytes = 0) {
     auto v = detail::to_c(descs, num_descs);
     detail::check("rmsnorm_linear_int4_fused",
                   xinfer_rmsnorm_linear_int4_fused_f16(detail::q(s), X, norm_weight, eps,
                                                        descs ? v.data() : nullptr, num_descs, M, K,
-                                                       group_size));
+                                                       group_size, workspace, workspace_bytes));
 }
 
 // rmsnorm + mlp_gate_up_swiglu_int4 in one call (forward.cpp:273-281)
 inline void rmsnorm_mlp_gate_up_swiglu_int4(hipStream_t s, half* Y, const half* X, const float* norm_weight,
                                             float eps, const uint8_t* W_gate, const half* scales_gate,
                                             const uint8_t* W_up, const half* scales_up, int64_t M,
-                                            int64_t N, int64_t K, int group_size = 128) {
+                                            int64_t N, int64_t K, int group_size = 128,
+                                            void* workspace = nullptr, size_t workspace_bytes = 0) {
     detail::check("rmsnorm_mlp_gate_up_swiglu_int4",
                   xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(detail::q(s), Y, X, norm_weight, eps, W_gate,
                                                              scales_gate, W_up, scales_up, M, N, K,
-                                                             group_size));
+                                                             group_size, workspace, workspace_bytes));
 }
 
 // linear_int4 + add_inplace in one call: residual += X W^T (+ bias)

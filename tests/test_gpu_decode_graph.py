@@ -58,20 +58,28 @@ def _buffers(M):
     f16 = dict(dtype=torch.float16, device="cuda")
     return dict(q=torch.empty((M, QD), **f16), k=torch.empty((M, KVD), **f16), v=torch.empty((M, KVD), **f16),
                 act=torch.empty((M, INTER), **f16), xn=torch.empty((M, H), **f16),
-                ids=torch.empty((M,), dtype=torch.int32, device="cuda"))
+                ids=torch.empty((M,), dtype=torch.int32, device="cuda"),
+                ws=torch.empty(M * H * 2, dtype=torch.uint8, device="cuda"),
+                lm=torch.empty(max(8, ops_mod().lm_head_argmax_scratch_size(M, VOCAB, H)), dtype=torch.uint8,
+                               device="cuda"))
+
+
+def ops_mod():
+    from xinfer_amd import ops
+    return ops
 
 
 def _step(ops, L, resid, b, M):
     """One decode step's projections; `resid` [M, H] is updated in place."""
     descs = [ops.FusedProjectionDesc(b[n], W, S, None, N)
              for n, (W, S), N in zip("qkv", L.dqkv, (QD, KVD, KVD))]
-    ops.rmsnorm_linear_int4_fused(resid, L.dln[0], 1e-6, descs, 3, M, H)
+    ops.rmsnorm_linear_int4_fused(resid, L.dln[0], 1e-6, descs, 3, M, H, workspace=b["ws"])
     ops.linear_int4_residual(resid, b["q"], L.do[0], L.do[1], None, M, H, QD)
     ops.rmsnorm_mlp_gate_up_swiglu_int4(b["act"], resid, L.dln[1], 1e-6, L.dg[0], L.dg[1], L.du[0], L.du[1],
-                                        M, INTER, H)
+                                        M, INTER, H, workspace=b["ws"])
     ops.linear_int4_residual(resid, b["act"], L.dd[0], L.dd[1], None, M, H, INTER)
     ops.rmsnorm(b["xn"], resid, L.dln[2], M, H, 1e-6)
-    ops.lm_head_argmax_int4(b["ids"], None, b["xn"], L.dlm[0], L.dlm[1], M, VOCAB, H)
+    ops.lm_head_argmax_int4(b["ids"], None, b["xn"], L.dlm[0], L.dlm[1], M, VOCAB, H, scratch=b["lm"])
 
 
 def _oracle_step(L, x_bits, M):
@@ -103,7 +111,7 @@ def test_decode_step_graph_replays_match_eager(M):
     x0 = oracle.f32_to_f16(np.random.default_rng(M).normal(0, 1, (M, H)).astype(np.float32))
     b = _buffers(M)
     resid = f16_dev(x0)
-    _step(ops, L, resid, b, M)  # eager (also allocates the library buffers of this shape)
+    _step(ops, L, resid, b, M)  # eager
     torch.cuda.synchronize()
     want_r, want_ids = to_np(resid).copy(), to_np(b["ids"]).copy()
 
@@ -135,7 +143,7 @@ def test_decode_step_graph_replays_match_eager(M):
         torch.cuda.synchronize()
         assert np.array_equal(to_np(resid), want_r), rep
         assert np.array_equal(to_np(b["ids"]), want_ids), rep
-        # eager work of another shape between replays (shares the library buffers)
+        # eager work between replays (same shapes, other buffers, the current stream)
         r2 = f16_dev(x0[:1].repeat(M, 0))
         _step(ops, L, r2, other, M)
         torch.cuda.synchronize()

@@ -39,6 +39,7 @@ EXPORTS = (
     "xinfer_dequant_int4_f32",
     "xinfer_rmsnorm_f16",
     "xinfer_add_inplace_f16",
+    "xinfer_rmsnorm_projection_workspace_bytes",
     "xinfer_rmsnorm_linear_int4_fused_f16",
     "xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16",
     "xinfer_linear_int4_residual_f16",
@@ -155,11 +156,13 @@ def load_library(path: str = None):
     L.xinfer_rmsnorm_f16.restype = ctypes.c_int
     L.xinfer_add_inplace_f16.argtypes = [_p, _p, _p, _i64]
     L.xinfer_add_inplace_f16.restype = ctypes.c_int
+    L.xinfer_rmsnorm_projection_workspace_bytes.argtypes = [_i64, _i64]
+    L.xinfer_rmsnorm_projection_workspace_bytes.restype = _sz
     L.xinfer_rmsnorm_linear_int4_fused_f16.argtypes = [_p, _p, _p, f32, ctypes.POINTER(FusedDesc), _i32,
-                                                       _i64, _i64, _i32]
+                                                       _i64, _i64, _i32, _p, _sz]
     L.xinfer_rmsnorm_linear_int4_fused_f16.restype = ctypes.c_int
     L.xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16.argtypes = [_p, _p, _p, _p, f32, _p, _p, _p, _p,
-                                                             _i64, _i64, _i64, _i32]
+                                                             _i64, _i64, _i64, _i32, _p, _sz]
     L.xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16.restype = ctypes.c_int
     L.xinfer_linear_int4_residual_f16.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32]
     L.xinfer_linear_int4_residual_f16.restype = ctypes.c_int

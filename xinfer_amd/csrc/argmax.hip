@@ -89,24 +89,37 @@ using namespace xhip;
 
 namespace xhip_host {
 
-// Library-owned scratch for callers that pass scratch == NULL: one buffer per
-// device, grown on demand and never freed while the process runs (a smaller
-// old buffer is kept alive because work already queued may still use it).
-void* library_scratch(size_t bytes) {
+// Library-owned scratch for callers that pass scratch == NULL: one buffer
+// per device and stream (so calls on different streams never share it),
+// grown on demand and never freed while the process runs (a smaller old
+// buffer is kept alive because work already queued may still use it).
+// Returns nullptr when the allocation fails or more than kStreams streams of
+// a device ask for one.
+void* library_scratch(hipStream_t st, size_t bytes) {
+    constexpr int kStreams = 16;
+    struct Entry { hipStream_t st; void* buf; size_t cap; };
     static std::mutex mu;
-    static void* buf[64] = {nullptr};
-    static size_t cap[64] = {0};
+    static Entry tab[64][kStreams];
+    static int n[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
     std::lock_guard<std::mutex> lock(mu);
-    if (cap[dev] < bytes) {
+    Entry* e = nullptr;
+    for (int i = 0; i < n[dev]; ++i)
+        if (tab[dev][i].st == st) e = &tab[dev][i];
+    if (!e) {
+        if (n[dev] == kStreams) return nullptr;
+        e = &tab[dev][n[dev]++];
+        *e = Entry{st, nullptr, 0};
+    }
+    if (e->cap < bytes) {
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes * 2;
         void* p = nullptr;
         if (hipMalloc(&p, want) != hipSuccess) return nullptr;
-        buf[dev] = p;
-        cap[dev] = want;
+        e->buf = p;
+        e->cap = want;
     }
-    return buf[dev];
+    return e->buf;
 }
 
 }  // namespace xhip_host
@@ -136,7 +149,7 @@ int xinfer_argmax_f32(void* stream, const float* logits, int64_t V, int64_t rows
     const int64_t nblk = (V + kArgSpan - 1) / kArgSpan;
     const size_t need = (size_t)(nblk * rows) * sizeof(ArgCand);
     if (!scratch) {
-        scratch = library_scratch(need);
+        scratch = library_scratch(st, need);
         if (!scratch) return XINFER_ERR_SCRATCH;
     } else if (scratch_bytes < need || !aligned(scratch, 8)) {
         return XINFER_ERR_SCRATCH;

@@ -122,8 +122,7 @@ std::string hex64(uint64_t v) {
 
 extern "C" {
 
-int xinfer_artifact_open(const char* filepath, xinfer_artifact** out, char* err, size_t err_len) {
-    if (!filepath || !out) return XINFER_ERR_INVALID_ARG;
+static int artifact_open_impl(const char* filepath, xinfer_artifact** out, char* err, size_t err_len) {
     *out = nullptr;
     xinfer_artifact* a = new xinfer_artifact();
     a->fd = open(filepath, O_RDONLY | O_CLOEXEC);
@@ -168,7 +167,8 @@ int xinfer_artifact_open(const char* filepath, xinfer_artifact** out, char* err,
         const uint64_t expect = (uint64_t)a->hdr.section_count * kEntryBytes;
         if (a->hdr.section_table_size != expect)
             return fail(a, err, err_len, "Section table size does not match section count.");
-        if (a->hdr.section_table_offset + a->hdr.section_table_size > fsize)
+        if (a->hdr.section_table_offset + a->hdr.section_table_size > fsize ||
+            a->hdr.section_table_offset + a->hdr.section_table_size < a->hdr.section_table_offset)
             return fail(a, err, err_len, "Section table points out of bounds.");
         a->secs.resize(a->hdr.section_count);
         if (!pread_all(a->fd, a->secs.data(), expect, a->hdr.section_table_offset))
@@ -184,6 +184,19 @@ int xinfer_artifact_open(const char* filepath, xinfer_artifact** out, char* err,
     }
     *out = a;
     return XINFER_OK;
+}
+
+// No C++ exception leaves the C ABI: a failed allocation while reading a
+// (possibly crafted) header becomes an I/O error.
+int xinfer_artifact_open(const char* filepath, xinfer_artifact** out, char* err, size_t err_len) {
+    if (!filepath || !out) return XINFER_ERR_INVALID_ARG;
+    *out = nullptr;
+    try {
+        return artifact_open_impl(filepath, out, err, err_len);
+    } catch (...) {
+        if (err && err_len) snprintf(err, err_len, "%s", "Out of memory while reading the container.");
+        return XINFER_ERR_IO;
+    }
 }
 
 void xinfer_artifact_close(xinfer_artifact* a) { delete a; }

@@ -890,42 +890,32 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
 
 // RMSNorm before a projection.  M = 1 (X staged whole by the GEMV): inside
 // the projection kernel, from the staged registers.  Otherwise the
-// standalone rmsnorm kernel writes the normalised rows to a per-device
-// library buffer that the projection then reads: measured faster at M >= 2
-// than a prologue inside the small-batch kernel (every block would repeat
-// the row reduction and the norm-weight reads before its first MFMA).
+// standalone rmsnorm kernel writes the normalised rows to the caller's
+// workspace (M * K fp16), which the projection then reads: measured faster
+// at M >= 2 than a prologue inside the small-batch kernel (every block would
+// repeat the row reduction and the norm-weight reads before its first MFMA).
 // Returns the X the projection reads and whether the kernel applies the norm.
+bool norm_in_projection(int64_t M, int64_t K) { return M == 1 && xhip_host::gemv_stages_x(1, K); }
+
 int norm_input(hipStream_t st, const void* X, const float* norm_w, float eps, int64_t M, int64_t K,
-               const void** Xp, bool* in_kernel) {
+               void* ws, size_t ws_bytes, const void** Xp, bool* in_kernel) {
     *Xp = X;
     *in_kernel = false;
     if (!norm_w) return XINFER_OK;
-    if (M == 1 && xhip_host::gemv_stages_x(1, K)) {
+    if (norm_in_projection(M, K)) {
         *in_kernel = true;
         return XINFER_OK;
     }
-    static std::mutex mu;
-    static void* buf[64] = {nullptr};
-    static size_t cap[64] = {0};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return XINFER_ERR_HIP;
-    const size_t need = (size_t)M * (size_t)K * 2;
-    {
-        std::lock_guard<std::mutex> lock(mu);
-        if (cap[dev] < need) {  // grown, never freed: queued work may still read the old one
-            void* p = nullptr;
-            if (hipMalloc(&p, need) != hipSuccess) return XINFER_ERR_SCRATCH;
-            buf[dev] = p;
-            cap[dev] = need;
-        }
-        *Xp = buf[dev];
-    }
-    return xinfer_rmsnorm_f16(st, const_cast<void*>(*Xp), X, norm_w, M, K, eps);
+    if (!ws || ws_bytes < (size_t)M * (size_t)K * 2) return XINFER_ERR_SCRATCH;
+    if (!xhip_host::aligned(ws, 16)) return XINFER_ERR_MISALIGNED;
+    *Xp = ws;
+    return xinfer_rmsnorm_f16(st, ws, X, norm_w, M, K, eps);
 }
 
 // linear_int4_fused with an optional RMSNorm on X first (norm_w != null).
 int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs, int32_t num_descs,
-                   int64_t M, int64_t K, int32_t group_size, const float* norm_w, float eps) {
+                   int64_t M, int64_t K, int32_t group_size, const float* norm_w, float eps,
+                   void* ws = nullptr, size_t ws_bytes = 0) {
     if (!descs || num_descs <= 0 || num_descs > 4) return XINFER_ERR_INVALID_ARG;
     if (M <= 0 || K <= 0) return XINFER_OK;
     if (!X0) return XINFER_ERR_INVALID_ARG;
@@ -940,7 +930,7 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
     }
     const void* X = X0;
     bool norm_in_kernel = false;
-    if (int rc = norm_input(st, X0, norm_w, eps, M, K, &X, &norm_in_kernel)) return rc;
+    if (int rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel)) return rc;
     GemvParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
@@ -988,7 +978,8 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
 
 int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate, const void* scales_gate,
                     const uint8_t* W_up, const void* scales_up, int64_t M, int64_t N, int64_t K,
-                    int32_t group_size, const float* norm_w, float eps) {
+                    int32_t group_size, const float* norm_w, float eps, void* ws = nullptr,
+                    size_t ws_bytes = 0) {
     if (M <= 0 || N <= 0 || K <= 0) return XINFER_OK;
     int rc = check_common(M, N, K, group_size);
     if (rc) return rc;
@@ -1000,7 +991,7 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const void* X = X0;
     bool norm_in_kernel = false;
-    if ((rc = norm_input(st, X0, norm_w, eps, M, K, &X, &norm_in_kernel))) return rc;
+    if ((rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel))) return rc;
     if (M >= 2 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
         if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc))
@@ -1053,21 +1044,29 @@ int xinfer_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
                            nullptr, 0.0f);
 }
 
+size_t xinfer_rmsnorm_projection_workspace_bytes(int64_t M, int64_t K) {
+    if (M <= 0 || K <= 0 || norm_in_projection(M, K)) return 0;
+    return (size_t)M * (size_t)K * 2;
+}
+
 int xinfer_rmsnorm_linear_int4_fused_f16(void* stream, const void* X, const float* norm_weight,
                                          float eps, const xinfer_fused_desc* descs, int32_t num_descs,
-                                         int64_t M, int64_t K, int32_t group_size) {
+                                         int64_t M, int64_t K, int32_t group_size, void* workspace,
+                                         size_t workspace_bytes) {
     if (!norm_weight) return XINFER_ERR_INVALID_ARG;
-    return fused_f16_impl(stream, X, descs, num_descs, M, K, group_size, norm_weight, eps);
+    return fused_f16_impl(stream, X, descs, num_descs, M, K, group_size, norm_weight, eps, workspace,
+                          workspace_bytes);
 }
 
 int xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(void* stream, void* Y, const void* X,
                                                const float* norm_weight, float eps,
                                                const uint8_t* W_gate, const void* scales_gate,
                                                const uint8_t* W_up, const void* scales_up, int64_t M,
-                                               int64_t N, int64_t K, int32_t group_size) {
+                                               int64_t N, int64_t K, int32_t group_size, void* workspace,
+                                               size_t workspace_bytes) {
     if (!norm_weight) return XINFER_ERR_INVALID_ARG;
     return swiglu_f16_impl(stream, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, group_size,
-                           norm_weight, eps);
+                           norm_weight, eps, workspace, workspace_bytes);
 }
 
 int xinfer_linear_int4_residual_f16(void* stream, void* residual, const void* X, const uint8_t* W_int4,
@@ -1092,14 +1091,17 @@ size_t xinfer_lm_head_argmax_scratch_bytes(int64_t M, int64_t N, int64_t K) {
 }  // extern "C"
 
 namespace xhip_host {
-void* library_scratch(size_t bytes);  // argmax.hip
+void* library_scratch(hipStream_t st, size_t bytes);  // argmax.hip
 }
 
-extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* logits,
-                                          const void* X, const uint8_t* W_int4,
-                                          const void* scales, int64_t M, int64_t N, int64_t K,
-                                          int32_t group_size, void* scratch,
-                                          size_t scratch_bytes) {
+namespace xhip_host {
+
+// LM head + argmax on candidate scratch `cand` of `cand_bytes` bytes; with
+// cand == NULL and library_ok, the library's per-stream buffer (allocated on
+// first use).
+int lm_head_argmax_impl(void* stream, int32_t* ids, float* logits, const void* X, const uint8_t* W_int4,
+                        const void* scales, int64_t M, int64_t N, int64_t K, int32_t group_size, void* cand,
+                        size_t cand_bytes, bool library_ok) {
     if (M <= 0 || N <= 0 || K <= 0) return XINFER_OK;
     if (M > 8) return XINFER_ERR_UNSUPPORTED;
     int rc = check_common(M, N, K, group_size);
@@ -1110,16 +1112,21 @@ extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* log
         !aligned(ids, 4))
         return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    auto get_parts = [&](size_t need, ArgCand** parts) {
+        if (!cand) {
+            if (!library_ok) return XINFER_ERR_SCRATCH;
+            cand = library_scratch(st, need);
+            if (!cand) return XINFER_ERR_SCRATCH;
+            cand_bytes = need;
+        }
+        if (cand_bytes < need || !aligned(cand, 8)) return XINFER_ERR_SCRATCH;
+        *parts = reinterpret_cast<ArgCand*>(cand);
+        return XINFER_OK;
+    };
     int nparts = 0;
     if (M >= 2 && !mb_argmax_plan(M, N, K, &nparts)) {
-        const size_t need = (size_t)M * (size_t)nparts * sizeof(ArgCand);
-        if (!scratch) {
-            scratch = library_scratch(need);
-            if (!scratch) return XINFER_ERR_SCRATCH;
-        } else if (scratch_bytes < need || !aligned(scratch, 8)) {
-            return XINFER_ERR_SCRATCH;
-        }
-        ArgCand* parts = reinterpret_cast<ArgCand*>(scratch);
+        ArgCand* parts = nullptr;
+        if (int src = get_parts((size_t)M * (size_t)nparts * sizeof(ArgCand), &parts)) return src;
         int mrc = XINFER_OK;
         if (!mb_argmax(st, logits, X, W_int4, scales, M, N, K, parts, &nparts, &mrc)) {
             if (mrc) return mrc;
@@ -1139,16 +1146,21 @@ extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* log
     p.d[0].N = (int32_t)N;
     const GemvPlan pl = plan_gemv<EPI_ARGMAX, float>(p, mr_for(M));
     const int blocks = pl.blocks;
-    const size_t need = (size_t)M * (size_t)blocks * sizeof(ArgCand);
-    if (!scratch) {
-        scratch = library_scratch(need);
-        if (!scratch) return XINFER_ERR_SCRATCH;
-    } else if (scratch_bytes < need || !aligned(scratch, 8)) {
-        return XINFER_ERR_SCRATCH;
-    }
-    p.parts = reinterpret_cast<ArgCand*>(scratch);
+    if (int src = get_parts((size_t)M * (size_t)blocks * sizeof(ArgCand), &p.parts)) return src;
     if (launch_plan<EPI_ARGMAX, float>(p, pl, st) || launch_status()) return XINFER_ERR_HIP;
     hipLaunchKernelGGL((argmax_finalize_kernel<int32_t>), dim3((unsigned)M), dim3(256), 0, st,
                        p.parts, (int32_t)blocks, ids);
     return launch_status();
 }
+
+}  // namespace xhip_host
+
+extern "C" int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* logits,
+                                          const void* X, const uint8_t* W_int4,
+                                          const void* scales, int64_t M, int64_t N, int64_t K,
+                                          int32_t group_size, void* scratch_buf,
+                                          size_t scratch_bytes) {
+    return xhip_host::lm_head_argmax_impl(stream, ids, logits, X, W_int4, scales, M, N, K, group_size, scratch_buf,
+                               scratch_bytes, true);
+}
+

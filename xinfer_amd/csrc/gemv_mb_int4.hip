@@ -27,8 +27,9 @@
 //     branch-free: rows past N and padding items read zeros without memory
 //     traffic).  Results go through LDS to a coalesced epilogue.
 //   * when K is long and N short (the down projection) the planner splits K
-//     over ks blocks per tile range.  Each writes its FP32 partial sums to a
-//     workspace; the last block of a range (device-scope counter) adds the
+//     over ks blocks per tile range.  Each writes its FP32 partial sums to
+//     the calling stream's split-K slot (a static device array, scratch.hip);
+//     the last block of a range (device-scope counter) adds the
 //     slices in slice order, so results do not depend on timing, and resets
 //     the counter for the next call.
 // Epilogues: bias + fp16/fp32 store, SiLU(gate) * up (paired tiles), and the
@@ -516,37 +517,6 @@ constexpr size_t kMaxLds = 160 * 1024;
 // 32-64 rows forces 5-10 k-slices and a large split-K combine.
 constexpr int kMaxMbM = 16;
 
-// Per-device workspace for split-K partial sums plus a zeroed counter array.
-// Grown on demand (outside any graph capture: the first call of a shape
-// allocates), never freed; counters are reset by the kernels themselves.
-constexpr size_t kMaxRanges = 1 << 16;
-bool mb_workspace(size_t ws_bytes, float** ws, uint32_t** cnt) {
-    static std::mutex mu;
-    static void* wbuf[64] = {nullptr};
-    static size_t wcap[64] = {0};
-    static uint32_t* cbuf[64] = {nullptr};
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-    std::lock_guard<std::mutex> lock(mu);
-    if (!cbuf[dev]) {
-        void* c = nullptr;
-        if (hipMalloc(&c, kMaxRanges * sizeof(uint32_t)) != hipSuccess) return false;
-        if (hipMemset(c, 0, kMaxRanges * sizeof(uint32_t)) != hipSuccess) return false;
-        if (hipDeviceSynchronize() != hipSuccess) return false;
-        cbuf[dev] = reinterpret_cast<uint32_t*>(c);
-    }
-    if (wcap[dev] < ws_bytes) {
-        const size_t want = ws_bytes < (4u << 20) ? (4u << 20) : ws_bytes;
-        void* w = nullptr;
-        if (hipMalloc(&w, want) != hipSuccess) return false;
-        wbuf[dev] = w;  // the previous buffer may still be read by queued work: kept
-        wcap[dev] = want;
-    }
-    *ws = reinterpret_cast<float*>(wbuf[dev]);
-    *cnt = cbuf[dev];
-    return true;
-}
-
 }  // namespace
 
 namespace xhip_host {
@@ -573,8 +543,15 @@ struct MbPlan {
 //   MR:  the m stride of the staged X (4, 8 or 16: M rounded up).
 bool gemv_stages_x(int64_t M, int64_t K);  // gemv_int4.hip
 
+// ws_cap / cnt_cap: the split-K slot available to this call (floats of
+// partials, tile-range counters); a plan that splits K beyond it is rejected.
+// raise_ok = false keeps ks at what the X slice needs (no extra slices for
+// short N), the retry when the raised plan does not fit the slot.
+bool splitk_slot(hipStream_t st, float** partials, size_t* partial_floats, uint32_t** counters,
+                 int* ncounters);  // scratch.hip
+
 template <int EPI, typename OutT>
-bool plan_mb(MbParams& p, MbPlan& pl) {
+bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise_ok) {
     const MbOverrides& ov = mb_overrides();
     const int M = p.M;
     // M = 2: the VALU GEMV measured faster while it stages all of X in LDS
@@ -633,7 +610,7 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
         tiles_blk = (tiles_total + rt - 1) / rt;
         ranges = 0;
         for (int i = 0; i < p.ndesc; ++i) ranges += ((p.d[i].N + 15) / 16 + tiles_blk - 1) / tiles_blk;
-        if (pass == 0 && ov.ks <= 0 && ov.raise != 0 && EPI != MB_ARGMAX && ranges * ks < target) {
+        if (pass == 0 && ov.ks <= 0 && ov.raise != 0 && raise_ok && EPI != MB_ARGMAX && ranges * ks < target) {
             int ks2 = (int)(target / ranges);
             if (ks2 > ng) ks2 = ng;
             if (ks2 > ks) { ks = ks2; continue; }
@@ -720,7 +697,7 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     while ((1 << lkw) < kw) ++lkw;
     const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16;
     if (lds > kMaxLds) return false;
-    if (ks > 1 && ranges > (int64_t)kMaxRanges) return false;
+    if (ks > 1 && ranges > cnt_cap) return false;
     for (int i = 0; ks > 1 && i < p.ndesc; ++i)  // 32-bit buffer offsets into the partials
         if ((int64_t)ks * (E * M * p.d[i].N + 64) * 4 >= (1LL << 31)) return false;
     pl.mr = mr;
@@ -751,6 +728,7 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
         p.ws_desc[i] = 0;
         p.ws_slice[i] = 0;
     }
+    if (ks > 1 && (size_t)wsoff > ws_cap) return false;
     pl.blocks = blocks;
     pl.ws_floats = ks > 1 ? (size_t)wsoff : 0;
     p.ks = ks;
@@ -761,12 +739,29 @@ bool plan_mb(MbParams& p, MbPlan& pl) {
     return true;
 }
 
+// Plan against the calling stream's split-K slot: the raised plan first,
+// then the plan with the fewest slices; with no slot (every slot owned by
+// another stream) only plans without a cross-block split are accepted.
+template <int EPI, typename OutT>
+bool plan_mb_stream(hipStream_t st, MbParams& p, MbPlan& pl) {
+    float* ws = nullptr;
+    uint32_t* cnt = nullptr;
+    size_t ws_cap = 0;
+    int ncnt = 0;
+    if (!splitk_slot(st, &ws, &ws_cap, &cnt, &ncnt)) {
+        ws = nullptr;
+        cnt = nullptr;
+        ws_cap = 0;
+        ncnt = 0;
+    }
+    p.ws = ws;
+    p.cnt = cnt;
+    return plan_mb<EPI, OutT>(p, pl, ws_cap, ncnt, true) || plan_mb<EPI, OutT>(p, pl, ws_cap, ncnt, false);
+}
+
 template <int EPI, typename OutT>
 int launch_mb(const MbParams& p0, const MbPlan& pl, hipStream_t st) {
     MbParams p = p0;
-    if (pl.ks > 1) {
-        if (!mb_workspace(pl.ws_floats * sizeof(float), &p.ws, &p.cnt)) return XINFER_ERR_SCRATCH;
-    }
     if (pl.lds > 64 * 1024) {
         static std::mutex mu;
         static const void* done[256];
@@ -803,7 +798,7 @@ int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void
         p.d[i].N = (int32_t)descs[i].N;
     }
     MbPlan pl;
-    const bool ok = y_f32 ? plan_mb<MB_PLAIN, float>(p, pl) : plan_mb<MB_PLAIN, f16>(p, pl);
+    const bool ok = y_f32 ? plan_mb_stream<MB_PLAIN, float>(st, p, pl) : plan_mb_stream<MB_PLAIN, f16>(st, p, pl);
     if (!ok) return 1;
     *rc = y_f32 ? launch_mb<MB_PLAIN, float>(p, pl, st) : launch_mb<MB_PLAIN, f16>(p, pl, st);
     return 0;
@@ -824,7 +819,7 @@ int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const v
     p.d[0].Y = Y;
     p.d[0].N = (int32_t)N;
     MbPlan pl;
-    if (!plan_mb<MB_SWIGLU, f16>(p, pl)) return 1;
+    if (!plan_mb_stream<MB_SWIGLU, f16>(st, p, pl)) return 1;
     *rc = launch_mb<MB_SWIGLU, f16>(p, pl, st);
     return 0;
 }
@@ -837,7 +832,7 @@ int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts) {
     p.ndesc = 1;
     p.d[0].N = (int32_t)N;
     MbPlan pl;
-    if (!plan_mb<MB_ARGMAX, float>(p, pl)) return 1;
+    if (!plan_mb<MB_ARGMAX, float>(p, pl, 0, 0, false)) return 1;
     *nparts = pl.nranges;
     return 0;
 }
@@ -863,7 +858,7 @@ int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, co
     p.d[0].Y = logits;
     p.d[0].N = (int32_t)N;
     MbPlan pl;
-    if (!plan_mb<MB_ARGMAX, float>(p, pl)) return 1;
+    if (!plan_mb<MB_ARGMAX, float>(p, pl, 0, 0, false)) return 1;
     *nparts = pl.nranges;
     *rc = launch_mb<MB_ARGMAX, float>(p, pl, st);
     return 0;

@@ -143,26 +143,46 @@ def add_inplace(a: torch.Tensor, b: torch.Tensor, num_elements: int, stream=None
     check("add_inplace", L.xinfer_add_inplace_f16(_stream(stream), _ptr(a), _ptr(b), num_elements))
 
 
+def rmsnorm_projection_workspace_size(M: int, K: int) -> int:
+    """Bytes of workspace the RMSNorm + projection calls need (0 at M = 1)."""
+    return int(load_library().xinfer_rmsnorm_projection_workspace_bytes(M, K))
+
+
+def _norm_workspace(X: torch.Tensor, M: int, K: int, workspace: Optional[torch.Tensor]):
+    """The caller's workspace, or a fresh torch buffer when none was given."""
+    if workspace is None:
+        need = rmsnorm_projection_workspace_size(M, K)
+        if need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=X.device)
+    nbytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    return _ptr(workspace), nbytes
+
+
 def rmsnorm_linear_int4_fused(X: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                               descs: Sequence[FusedProjectionDesc], num_descs: int, M: int, K: int,
-                              group_size: int = 128, stream=None) -> None:
-    """rmsnorm(X) then linear_int4_fused, in one launch (decode: M <= 8)."""
+                              group_size: int = 128, workspace: Optional[torch.Tensor] = None,
+                              stream=None) -> None:
+    """rmsnorm(X) then linear_int4_fused (one launch at M = 1; at M >= 2 the
+    normalised rows go through `workspace`, allocated here when not given)."""
     L = load_library()
+    ws, nws = _norm_workspace(X, M, K, workspace)
     arr = (FusedDesc * max(1, num_descs))()
     for i in range(min(num_descs, len(descs))):
         d = descs[i]
         arr[i] = FusedDesc(_ptr(d.Y), _ptr(d.W_int4), _ptr(d.scales), _ptr(d.bias), d.N)
     check("rmsnorm_linear_int4_fused", L.xinfer_rmsnorm_linear_int4_fused_f16(
-        _stream(stream), _ptr(X), _ptr(norm_weight), float(eps), arr, num_descs, M, K, group_size))
+        _stream(stream), _ptr(X), _ptr(norm_weight), float(eps), arr, num_descs, M, K, group_size,
+        ws, nws))
 
 
 def rmsnorm_mlp_gate_up_swiglu_int4(Y, X, norm_weight, eps, W_gate, scales_gate, W_up, scales_up,
-                                    M, N, K, group_size=128, stream=None) -> None:
-    """rmsnorm(X) then mlp_gate_up_swiglu_int4, in one launch (decode: M <= 8)."""
+                                    M, N, K, group_size=128, workspace=None, stream=None) -> None:
+    """rmsnorm(X) then mlp_gate_up_swiglu_int4 (workspace as rmsnorm_linear_int4_fused)."""
     L = load_library()
+    ws, nws = _norm_workspace(X, M, K, workspace)
     check("rmsnorm_mlp_gate_up_swiglu_int4", L.xinfer_rmsnorm_mlp_gate_up_swiglu_int4_f16(
         _stream(stream), _ptr(Y), _ptr(X), _ptr(norm_weight), float(eps), _ptr(W_gate), _ptr(scales_gate),
-        _ptr(W_up), _ptr(scales_up), M, N, K, group_size))
+        _ptr(W_up), _ptr(scales_up), M, N, K, group_size, ws, nws))
 
 
 def linear_int4_residual(residual: torch.Tensor, X, W_int4, scales, bias, M, N, K, group_size=128,
