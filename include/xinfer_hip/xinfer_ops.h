@@ -197,6 +197,20 @@ int xinfer_lm_head_argmax_int4(void* stream, int32_t* ids, float* logits,
                                int64_t K, int32_t group_size, void* scratch,
                                size_t scratch_bytes);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under hipGraph capture, serving loops or harnesses that forbid
+ * hipMalloc): xinfer_lm_head_argmax_int4 with the per-block argmax
+ * candidates in a static device array of the library (128 KiB per device)
+ * instead of caller scratch; no allocation on any call.  Shapes that need
+ * more candidates than the array holds return XINFER_ERR_SCRATCH (M <= 8
+ * at any vocab size fits today).  All calls on one device share the array:
+ * calls that overlap on one device (other streams, concurrent graph
+ * replays) race. */
+int xinfer_lm_head_argmax_int4_noalloc(void* stream, int32_t* ids, float* logits,
+                                       const void* X, const uint8_t* W_int4,
+                                       const void* scales, int64_t M, int64_t N,
+                                       int64_t K, int32_t group_size);
+
 /* ---------------------------------------------------------------------------
  * Dequantise: out[n][k] = fp32(q[n][k]) * fp32(S[n][k/G]) (exact in FP32).
  * Replaces the converter's `dequantize_int4_symmetric` oracle

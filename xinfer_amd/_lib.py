@@ -36,6 +36,7 @@ EXPORTS = (
     "xinfer_argmax_f32",
     "xinfer_lm_head_argmax_scratch_bytes",
     "xinfer_lm_head_argmax_int4",
+    "xinfer_lm_head_argmax_int4_noalloc",
     "xinfer_dequant_int4_f32",
     "xinfer_rmsnorm_f16",
     "xinfer_add_inplace_f16",
@@ -149,6 +150,8 @@ def load_library(path: str = None):
     L.xinfer_lm_head_argmax_int4.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32,
                                              _p, _sz]
     L.xinfer_lm_head_argmax_int4.restype = ctypes.c_int
+    L.xinfer_lm_head_argmax_int4_noalloc.argtypes = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32]
+    L.xinfer_lm_head_argmax_int4_noalloc.restype = ctypes.c_int
     L.xinfer_dequant_int4_f32.argtypes = [_p, _p, _p, _p, _i64, _i64, _i32]
     L.xinfer_dequant_int4_f32.restype = ctypes.c_int
     f32 = ctypes.c_float
