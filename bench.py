@@ -442,7 +442,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         record("cfg4_prefill_m512_n17408_k5120",
                {"M": M, "N": N, "K": K, "us": round(e * 1e6, 2), "TFLOPs": round(fl / e / 1e12, 1),
                 "frac_fp16_mfma": round(fl / e / 1e12 / FP16_PEAK_TFLOPS, 4),
-                "kernel": "xhip::gemm_int4_mfma_kernel<NQ=2,NR=1>"})
+                "kernel": "xhip::gemm_ws_int4_kernel (256x136 blocks, producer/consumer waves)"})
     return out
 
 

@@ -401,6 +401,12 @@ def test_prefill_gemm_shapes(M, N, K):
     print(_linear_case(M, N, K, seed=M + N))
 
 
+@pytest.mark.parametrize("M,N,K", [(128, 272, 1024), (130, 300, 384 * 8), (512, 4352, 5120)])
+def test_prefill_gemm_f32_out_exact(M, N, K):
+    """fp32-output GEMM (exact q, FP32 group scale), incl. a leftover tile."""
+    print(_linear_case(M, N, K, seed=M + 3, out="f32"))
+
+
 def test_prefill_gemm_f32_out_and_bias():
     import torch
     ops = _ops()
@@ -411,9 +417,10 @@ def test_prefill_gemm_f32_out_and_bias():
     Y = _empty((M, N), torch.float32)
     ops.linear_int4(Y, f16_dev(Xb), to_dev(W), f16_dev(S), to_dev(bias), M, N, K)
     ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, bias=bias, nthreads=cpu_threads())
+    # fp32 output: exact q, FP32 group scale, the reference's fp32-out bound
+    # (tests/test_ops_oracle.cpp:781)
     err = np.abs(to_np(Y) - ref).max()
-    # q*s is rounded to fp16 on the MFMA path: bound it like the fp16 outputs
-    assert err <= 1e-2 and kat.rel_l2(to_np(Y), ref) <= 1e-3, err
+    assert err <= 1e-4 * max(1.0, np.abs(ref).max()) and kat.rel_l2(to_np(Y), ref) <= 1e-4, err
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 256, 512), (40, 200, 1024), (512, 17408 // 8, 5120)])

@@ -19,7 +19,7 @@ BUILD_DIR = os.path.join(ROOT, "_build")
 ARCH = "gfx950"
 
 SOURCES = ["gemv_int4.hip", "gemv_pair_int4.hip", "gemv_mb_int4.hip", "argmax.hip", "misc.hip", "gemm_int4.hip", "crc64.hip",
-           "artifact.hip", "scratch.hip", "noalloc.hip"]
+           "artifact.hip", "scratch.hip", "noalloc.hip", "gemm_ws_int4.hip"]
 
 # -packed-fp32-ops: keep the compiler from forming v_pk_{add,mul,fma}_f32
 # (packed fp16 ops are unaffected).

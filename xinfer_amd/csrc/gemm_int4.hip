@@ -30,6 +30,7 @@
 #include <stdlib.h>
 
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 
@@ -89,10 +90,25 @@ __device__ __forceinline__ void dma16(const void* g, unsigned char* lds_wave_bas
 
 constexpr int kWavesG = 8;   // waves per GEMM block (2 per SIMD)
 
-template <int NQ, int NR, int EPI, typename OutT>
+// Waves: wave w owns weight tiles w*NQ .. w*NQ+NQ-1 for all 8 M-tiles (the
+// decoded B operand of a tile feeds 8 MFMAs).  The NR = 1 leftover tile is
+// split over k instead of M: wave w computes all 8 M-tiles of it at the
+// k-steps s with s % 8 == w, so its B operand also feeds 8 MFMAs (split over
+// M, each wave decoded it for one MFMA: a third of the decode work for 1/17
+// of the MFMAs).  In every group four waves, one per SIMD, take one leftover
+// k-step.  The waves' partial sums of the leftover tile meet in LDS after the
+// loop and are added in wave order.
+//
+// EXACT: the B operand is the exact fp16 integer q; the four k-steps of a
+// group accumulate q*x in FP32 partial sums, which are then scaled by the
+// fp32 group scale into the totals (sum_g s_g * sum_k x q, the reference's
+// arithmetic; costs one FP32 FMA per output and group and the registers of
+// the partial sums).  Otherwise B = fp16(q * s).
+template <int NQ, int NR, int EPI, typename OutT, bool EXACT>
 __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p) {
     constexpr bool SWIGLU = (EPI == 1);
     static_assert(!SWIGLU || NR == 0, "SwiGLU tiles pair gate/up per wave");
+    static_assert(NR <= 1, "one leftover tile at most");
     constexpr int NW = kWavesG;
     constexpr int NT = SWIGLU ? 2 * NW * NQ : NW * NQ + NR;  // weight tiles (16 rows) per block
     constexpr int OWN = SWIGLU ? 2 * NQ : NQ;                // full-M tiles per wave
@@ -100,11 +116,11 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
     constexpr int X_BYTES = kGM * 128 * 2;                   // 32 KB
     constexpr int W_BYTES = (NT + 1) * 1024;                 // + one shared spare slot
     constexpr int STAGE = X_BYTES + W_BYTES;
-    constexpr int NSC = OWN + NR;                            // B operands per wave per step
     constexpr int SROWS = 16 * NT;                           // weight rows of the block
     constexpr int SWL = (SROWS + 64 * NW - 1) / (64 * NW);  // scale DMA loads per wave per chunk
     constexpr int SC_BYTES = SROWS * 16;                     // one 8-group scale chunk
     constexpr int XPW = 32 / NW;                             // X DMA loads per wave per group
+    constexpr int ABUF = EXACT ? 1 : 2;                      // A operand sets in registers
 
     extern __shared__ __align__(16) unsigned char smem[];
 
@@ -134,8 +150,9 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
     const size_t row_bytes = (size_t)(K >> 1);
 
     // --- DMA sources (per lane, group 0) -------------------------------------
-    // X: wave-load wl (0..31) covers chunk q = wl*64 + lane of the layout
-    // [t][mt][lj][li] (16 bytes = 8 consecutive k of one row).
+    // X: wave-load wl (0..31) covers the 1 KB chunk (k-step t, M-tile mt):
+    // lane (lj, li) holds 8 consecutive k (32*lj + 8*t ..) of row 16*mt + li,
+    // the A-operand layout of v_mfma_f32_16x16x32_f16 for k-step t.
     const f16* xsrc[XPW];
 #pragma unroll
     for (int i = 0; i < XPW; ++i) {
@@ -177,16 +194,14 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
         const uint16_t* base = (SWIGLU && wb == p.W2) ? p.S2 : p.S;
         ssrc[i] = base + (size_t)row * ng;
     }
-    // LDS slots of the tiles this wave decodes: own full tiles, then leftovers
-    int wslot[NSC];
+    // LDS slots of the tiles this wave decodes
+    int wslot[OWN > 0 ? OWN : 1];
 #pragma unroll
-    for (int i = 0; i < NSC; ++i) {
+    for (int i = 0; i < OWN; ++i) {
         if (SWIGLU) wslot[i] = (i < NQ) ? wave * NQ + i : NW * NQ + wave * NQ + (i - NQ);
-        else wslot[i] = i < NQ ? wave * NQ + i : NW * NQ + (i - NQ);
+        else wslot[i] = wave * NQ + i;
     }
-    int sslot[NSC];
-#pragma unroll
-    for (int i = 0; i < NSC; ++i) sslot[i] = (wslot[i] * 16 + li) * 16;
+    constexpr int LSLOT = NW * NQ;  // the leftover tile
 
     auto issue_dma = [&](int g, int stage) {
         unsigned char* st = smem + stage * STAGE;
@@ -212,14 +227,15 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
     };
     constexpr int DPG = XPW + WPW;  // DMA loads per wave per group
 
-    f32x4 acc[8][OWN > 0 ? OWN : 1];
-    f32x4 accL[NR > 0 ? NR : 1];
+    const f32x4 zero4 = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[8][OWN > 0 ? OWN : 1];   // totals of the own tiles
+    f32x4 lac[8];                       // this wave's k-share of the leftover tile
 #pragma unroll
-    for (int mt = 0; mt < 8; ++mt)
+    for (int mt = 0; mt < 8; ++mt) {
 #pragma unroll
-        for (int i = 0; i < (OWN > 0 ? OWN : 1); ++i) acc[mt][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < (NR > 0 ? NR : 1); ++r) accL[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < (OWN > 0 ? OWN : 1); ++i) acc[mt][i] = zero4;
+        lac[mt] = zero4;
+    }
 
     issue_scale_chunk(0);
     issue_dma(0, 0);
@@ -228,45 +244,91 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
     auto make_b = [&](const u32x4& w, int t, f16x2 s2) -> f16x8 {
         f16x2 q[4];
         decode8_natural(w[t], q);
-        q[0] *= s2;
-        q[1] *= s2;
-        q[2] *= s2;
-        q[3] *= s2;
+        if (!EXACT) {
+            q[0] *= s2;
+            q[1] *= s2;
+            q[2] *= s2;
+            q[3] *= s2;
+        }
         return pack8(q);
     };
 
-    // One group = 4 k-steps; per step the wave issues 8*OWN + NR MFMAs.
-    // Leftover tile r: this wave does M-tile `wave` only.
+    // One group = 4 k-steps of 32; per step the wave issues 8*OWN MFMAs, plus
+    // 8 for the leftover tile at its k-step.  A operands of step t+1 are read
+    // from LDS while the MFMAs of step t run (ABUF = 2).
     auto compute_group = [&](int stage, int g) {
         const unsigned char* st = smem + stage * STAGE;
         const unsigned char* sc = sbuf + ((g >> 3) & 1) * SC_BYTES + (g & 7) * 2;
-        u32x4 wv[NSC];
-        f16x2 s2[NSC];
+        u32x4 wv[OWN > 0 ? OWN : 1];
+        f16 sh[OWN > 0 ? OWN : 1];
 #pragma unroll
-        for (int i = 0; i < NSC; ++i) {
+        for (int i = 0; i < OWN; ++i) {
             wv[i] = *reinterpret_cast<const u32x4*>(st + X_BYTES + wslot[i] * 1024 + lane * 16);
-            const f16 s = *reinterpret_cast<const f16*>(sc + sslot[i]);
-            s2[i] = f16x2{s, s};
+            sh[i] = *reinterpret_cast<const f16*>(sc + (wslot[i] * 16 + li) * 16);
         }
+        // leftover k-step of this wave in this group: (4g + t) % 8 == wave
+        const int tl = NR ? ((wave - 4 * g) & 7) : 8;
+        u32x4 wl = {0u, 0u, 0u, 0u};
+        f16 slh = (f16)0.0f;
+        if (NR) {
+            wl = *reinterpret_cast<const u32x4*>(st + X_BYTES + LSLOT * 1024 + lane * 16);
+            slh = *reinterpret_cast<const f16*>(sc + (LSLOT * 16 + li) * 16);
+        }
+        f32x4 part[8][OWN > 0 ? OWN : 1];  // EXACT: this group's unscaled sums
+        f16x8 a[ABUF][8];
+#pragma unroll
+        for (int mt = 0; mt < 8; ++mt) a[0][mt] = *reinterpret_cast<const f16x8*>(st + mt * 1024 + lane * 16);
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const unsigned char* xt = st + (t * 8) * 1024 + lane * 16;
-            f16x8 a[8];
-            if (OWN > 0) {
+            const int cur = ABUF == 2 ? (t & 1) : 0;
+            if (ABUF == 2 && t < 3) {
 #pragma unroll
-                for (int mt = 0; mt < 8; ++mt) a[mt] = *reinterpret_cast<const f16x8*>(xt + mt * 1024);
+                for (int mt = 0; mt < 8; ++mt)
+                    a[cur ^ 1][mt] = *reinterpret_cast<const f16x8*>(st + ((t + 1) * 8 + mt) * 1024 + lane * 16);
+            } else if (ABUF == 1 && t > 0) {
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt)
+                    a[0][mt] = *reinterpret_cast<const f16x8*>(st + (t * 8 + mt) * 1024 + lane * 16);
             }
-            f16x8 aw = *reinterpret_cast<const f16x8*>(xt + wave * 1024);
 #pragma unroll
-            for (int i = 0; i < NSC; ++i) {
-                const f16x8 bop = make_b(wv[i], t, s2[i]);
-                if (i < OWN) {
+            for (int i = 0; i < OWN; ++i) {
+                const f16x8 bop = make_b(wv[i], t, f16x2{sh[i], sh[i]});
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt) {
+                    if (EXACT)
+                        part[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][mt], bop, t == 0 ? zero4 : part[mt][i], 0, 0, 0);
+                    else
+                        acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][mt], bop, acc[mt][i], 0, 0, 0);
+                }
+            }
+            if (NR && t == tl) {
+                // a real branch: speculated, the 8 MFMAs and the decode
+                // would run at every k-step
+                asm volatile("" ::: "memory");
+                const f16x8 bop = make_b(wl, t, f16x2{slh, slh});
+                if (EXACT) {
+                    const float sl = (float)slh;
+#pragma unroll
+                    for (int mt = 0; mt < 8; ++mt) {
+                        const f32x4 q = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][mt], bop, zero4, 0, 0, 0);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) lac[mt][e] = __builtin_fmaf(sl, q[e], lac[mt][e]);
+                    }
+                } else {
 #pragma unroll
                     for (int mt = 0; mt < 8; ++mt)
-                        acc[mt][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], bop, acc[mt][i], 0, 0, 0);
-                } else {
-                    accL[i - OWN] = __builtin_amdgcn_mfma_f32_16x16x32_f16(aw, bop, accL[i - OWN], 0, 0, 0);
+                        lac[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[cur][mt], bop, lac[mt], 0, 0, 0);
                 }
+            }
+        }
+        if (EXACT) {
+#pragma unroll
+            for (int i = 0; i < OWN; ++i) {
+                const float s = (float)sh[i];
+#pragma unroll
+                for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[mt][i][e] = __builtin_fmaf(s, part[mt][i][e], acc[mt][i][e]);
             }
         }
     };
@@ -329,12 +391,25 @@ __global__ __launch_bounds__(512) void gemm_int4_mfma_kernel(const GemmParams p)
             }
         }
     }
+    if (NR) {
+        // the waves' k-shares of the leftover tile, added in wave order
+        __syncthreads();  // every wave is done with the stage buffers
+        f32x4* red = reinterpret_cast<f32x4*>(smem);
 #pragma unroll
-    for (int r = 0; r < NR; ++r) {
-        const int n = n0 + (NW * NQ + r) * 16 + li;
+        for (int mt = 0; mt < 8; ++mt) red[(wave * 8 + mt) * 64 + lane] = lac[mt];
+        __syncthreads();
+        const int mt = tid >> 6;  // 512 threads = 8 M-tiles x 64 lanes
+        f32x4 v = red[mt * 64 + lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const f32x4 o = red[(w * 8 + mt) * 64 + lane];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] += o[e];
+        }
+        const int n = n0 + LSLOT * 16 + li;
         const float bn = bias_of(n);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) store(m0 + wave * 16 + 4 * lj + e, n, accL[r][e] + bn);
+        for (int e = 0; e < 4; ++e) store(m0 + mt * 16 + 4 * lj + e, n, v[e] + bn);
     }
 }
 
@@ -352,13 +427,20 @@ struct GemmCfg {
     int nq, nr;
 };
 
-template <int EPI, typename OutT>
+// EXACT keeps a second set of accumulators (the group's unscaled sums): it
+// fits the registers with one own tile per wave only (NQ = 1, no SwiGLU).
+template <int EPI, typename OutT, bool EXACT>
 GemmKernel gemm_kernel_for(int nq, int nr) {
-    if (EPI == 1) return gemm_int4_mfma_kernel<1, 0, 1, OutT>;
-    if (nq == 2 && nr == 1) return gemm_int4_mfma_kernel<2, 1, 0, OutT>;
-    if (nq == 2) return gemm_int4_mfma_kernel<2, 0, 0, OutT>;
-    if (nq == 1) return gemm_int4_mfma_kernel<1, 0, 0, OutT>;
-    return gemm_int4_mfma_kernel<0, 4, 0, OutT>;
+    if constexpr (EXACT) {
+        if (EPI == 1) return nullptr;
+        return nr ? gemm_int4_mfma_kernel<1, 1, 0, OutT, true> : gemm_int4_mfma_kernel<1, 0, 0, OutT, true>;
+    } else {
+        if (EPI == 1) return gemm_int4_mfma_kernel<1, 0, 1, OutT, false>;
+        if (nq == 2 && nr == 1) return gemm_int4_mfma_kernel<2, 1, 0, OutT, false>;
+        if (nq == 2) return gemm_int4_mfma_kernel<2, 0, 0, OutT, false>;
+        if (nq == 1 && nr == 1) return gemm_int4_mfma_kernel<1, 1, 0, OutT, false>;
+        return gemm_int4_mfma_kernel<1, 0, 0, OutT, false>;
+    }
 }
 
 size_t gemm_lds_bytes(int nt) {
@@ -374,10 +456,19 @@ int launch_gemm(hipStream_t st, GemmParams& p) {
     // tiles 125 us; the leftover tile's extra A read makes 17 tiles cost more
     // than 16/17 of them would suggest).
     const int cus = xhip_host::num_cus();
-    const GemmCfg cands_plain[] = {{2, 1}, {2, 0}, {1, 0}, {0, 4}};
-    const double block_cost_plain[] = {1.21, 1.0, 0.66, 1.37};
+    const GemmCfg cands_plain[] = {{2, 1}, {2, 0}, {1, 1}, {1, 0}};
+    const double block_cost_plain[] = {1.04, 1.0, 0.70, 0.66};
     const GemmCfg cands_swiglu[] = {{1, 0}};
     const GemmCfg* cands = EPI == 1 ? cands_swiglu : cands_plain;
+    // fp32 outputs keep the reference's arithmetic (exact q, fp32 group
+    // scale; one own tile per wave); fp16 outputs use B = fp16(q * s).
+    // XINFER_GEMM_EXACT=0/1 forces one for the plain projection (tuning).
+    static const int force_exact = [] {
+        const char* v = getenv("XINFER_GEMM_EXACT");
+        return (v && *v) ? atoi(v) : -1;
+    }();
+    const bool exact = EPI != 1 && (force_exact >= 0 ? force_exact != 0 : std::is_same<OutT, float>::value);
+    const int cfirst = exact ? 2 : 0;  // exact: the NQ = 1 candidates
     const int ncand = EPI == 1 ? 1 : 4;
     const int mblocks = (p.M + kGM - 1) / kGM;
     GemmCfg best = cands[0];
@@ -386,8 +477,8 @@ int launch_gemm(hipStream_t st, GemmParams& p) {
         const char* v = getenv("XINFER_GEMM_CFG");
         return (v && *v) ? atoi(v) : -1;
     }();
-    for (int i = 0; i < ncand; ++i) {
-        if (forced >= 0 && forced < ncand) {
+    for (int i = cfirst; i < ncand; ++i) {
+        if (forced >= cfirst && forced < ncand) {
             best = cands[forced];
             break;
         }
@@ -404,7 +495,8 @@ int launch_gemm(hipStream_t st, GemmParams& p) {
     p.nranges = (p.N + ncol - 1) / ncol;
     const int blocks = p.mblocks * p.nranges;
     p.xcd_map = (8 % p.mblocks == 0) && (blocks % 8 == 0) ? 1 : 0;
-    GemmKernel k = gemm_kernel_for<EPI, OutT>(best.nq, best.nr);
+    GemmKernel k = exact ? gemm_kernel_for<EPI, OutT, true>(best.nq, best.nr)
+                         : gemm_kernel_for<EPI, OutT, false>(best.nq, best.nr);
     const size_t lds = gemm_lds_bytes(nt_w);
     static std::mutex mu;
     static GemmKernel configured[16];
@@ -453,9 +545,16 @@ int gemm_by_gemv_slabs(hipStream_t st, void* Y, bool y_f32, const void* X, const
     return XINFER_OK;
 }
 
+int gemm_ws_linear(hipStream_t st, void* Y, const void* X, const uint8_t* W, const uint16_t* S,
+                   const float* bias, int64_t M, int64_t N, int64_t K, bool residual, int* rc);  // gemm_ws_int4.hip
+
 int gemm_int4_f16(hipStream_t st, void* Y, bool y_f32, const void* X, const uint8_t* W,
                   const uint16_t* S, const uint8_t* W2, const uint16_t* S2, const float* bias,
                   int64_t M, int64_t N, int64_t K, bool residual) {
+    if (!y_f32 && !W2) {  // fp16 projection: the producer/consumer kernel where it fills the CUs
+        int rc = XINFER_OK;
+        if (!gemm_ws_linear(st, Y, X, W, S, bias, M, N, K, residual, &rc)) return rc;
+    }
     if (K % 1024 != 0) return gemm_by_gemv_slabs(st, Y, y_f32, X, W, S, W2, S2, bias, M, N, K, residual);
     GemmParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
