@@ -128,6 +128,62 @@ def _time_graph(torch, launch, steps, warmup, copies):
     return wall / n, e0.elapsed_time(e1) * 1e-3 / n, n
 
 
+def time_exact(torch, launch, steps, warmup, copies):
+    """The headline timing: exactly `steps` launches (rotating the weight
+    copies) captured in one HIP graph.  Untimed: `warmup` launches' worth of
+    replays (and at least MIN_WARM_S of work).  Timed: one replay of the
+    `steps` launches, synchronized on both sides, by the host clock and by
+    events on the replay stream.  Then 9 more replays, each timed by events:
+    their median per launch is reported beside the mean of the timed one.
+    Also returns the event time of one launch from cold: code loaded, the
+    Infinity Cache flushed by a 512 MiB fill, the GPU idle for 50 ms."""
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    launch(1 % copies)  # loads the code object
+    flush = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    flush.fill_(1)
+    torch.cuda.synchronize()
+    del flush
+    time.sleep(0.05)
+    e0.record(st)
+    launch(0)
+    e1.record(st)
+    torch.cuda.synchronize()
+    cold = e0.elapsed_time(e1) * 1e-3
+    for i in range(copies):
+        launch(i % copies)                          # warm up outside capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                launch(i % copies)
+    t0 = time.perf_counter()
+    done = 0
+    while done < warmup or time.perf_counter() - t0 < MIN_WARM_S:
+        g.replay()
+        done += steps
+        torch.cuda.synchronize()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record(st)
+    g.replay()
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ev = e0.elapsed_time(e1) * 1e-3
+    per = []
+    for _ in range(9):
+        e0.record(st)
+        g.replay()
+        e1.record(st)
+        torch.cuda.synchronize()
+        per.append(e0.elapsed_time(e1) * 1e-3 / steps)
+    per.sort()
+    return wall / steps, ev / steps, per[len(per) // 2], cold
+
+
 def time_launches(torch, launch, steps, warmup, copies, graph=False):
     """(wall s/step, event s/step) for `steps` launches rotating weight copies.
     graph=True captures one rotation into a HIP graph and times replays.
@@ -217,12 +273,18 @@ def main():
             W, S = rig.W[i], rig.S[i]
             ops.mlp_gate_up_swiglu_int4(Y, X, W[:N], S[:N], W[N:], S[N:], M, N, K)
 
-        wall_step, ev_step = time_launches(torch, launch_cfg1, args.steps, args.warmup,
-                                           rig.copies, graph=graph)
-        head = (wall_step, ev_step, rig.copies)
-        log(f"config 1: M={M} K={K} N=2x{N}, {rig.copies} weight copies, "
-            f"wall {wall_step*1e6:.2f} us/step, events {ev_step*1e6:.2f} us/launch, "
-            f"{nbytes/ev_step/1e9:.0f} GB/s")
+        if graph:
+            wall_step, ev_step, ev_med, cold = time_exact(torch, launch_cfg1, args.steps, args.warmup,
+                                                          rig.copies)
+        else:
+            wall_step, ev_step = time_launches(torch, launch_cfg1, args.steps, args.warmup,
+                                               rig.copies, graph=False)
+            ev_med, cold = ev_step, None
+        head = (wall_step, ev_step, rig.copies, ev_med, cold)
+        log(f"config 1: M={M} K={K} N=2x{N}, {rig.copies} weight copies, {args.steps} launches timed, "
+            f"wall {wall_step*1e6:.2f} us/step, events {ev_step*1e6:.2f} us/launch "
+            f"(median of 9 more replays {ev_med*1e6:.2f}), {nbytes/ev_step/1e9:.0f} GB/s; "
+            f"first launch (cold) {cold*1e6 if cold else float('nan'):.1f} us")
         del rig
 
     suite = {} if args.quick else run_suite(torch, dev, ops, synth, args, log, want, graph)
@@ -234,7 +296,7 @@ def main():
     if head is None:
         print(json.dumps({"suite": suite}), flush=True)
         return
-    wall_step, ev_step, copies = head
+    wall_step, ev_step, copies, ev_med, cold = head
     value = nbytes / wall_step / 1e9
     achieved = nbytes / ev_step / 1e9
     traffic = None
@@ -262,9 +324,14 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic,
+                     "traffic_source": "profiles/traffic_config1_gate_up_m1.json: committed rocprofv3 --pmc "
+                                       "FETCH_SIZE + WRITE_SIZE of this kernel, scaled by a plain copy "
+                                       "of known size (not measured in this run)",
                      "kernel": "xhip::gemv_int4_kernel<MR=1,R=2,EPI_SWIGLU,...,PF=1,NWV=8>",
                      "algorithmic_bytes_per_launch": nbytes,
-                     "avg_launch_us": round(ev_step * 1e6, 3)},
+                     "avg_launch_us": round(ev_step * 1e6, 3),
+                     "median_launch_us_9_replays": round(ev_med * 1e6, 3),
+                     "cold_first_launch_us": round(cold * 1e6, 2) if cold else None},
         "cpu_baseline": cpu,
         "suite": suite,
     }
@@ -475,8 +542,18 @@ def cpu_baseline(nbytes, log):
     v, dt, reps = res[cores]
     model = ""
     try:
+        info = {}
         with open("/proc/cpuinfo") as f:
-            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+            for ln in f:
+                if ":" in ln:
+                    k_, v_ = ln.split(":", 1)
+                    info.setdefault(k_.strip(), v_.strip())
+                if not ln.strip() and info:
+                    break
+        model = info.get("model name", "")
+        # family / model / stepping identify the part when the name is generic
+        model += " (family %s, model %s, stepping %s)" % (info.get("cpu family", "?"), info.get("model", "?"),
+                                                         info.get("stepping", "?"))
     except OSError:
         pass
     log(f"  cpu: {model} ({os.cpu_count()} logical cpus on the host, {cores} used)")
