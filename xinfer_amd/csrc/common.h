@@ -71,6 +71,21 @@ __device__ __forceinline__ void decode16_biased(uint32_t w0, uint32_t w1, f16x2 
     h[7] = as_h2((b8 & 0x00F000F0u) ^ 0x64806480u);
 }
 
+// Natural nibble order: byte b of w -> (k_2b, k_2b+1) as exact fp16
+// integers (byte permute, one v_bitop3_b32, one packed fma), times the
+// group scale.
+__device__ __forceinline__ void decode8_natural_scaled(uint32_t w, f16x2 s2, uint32_t out[4]) {
+    const f16x2 kMul = {(f16)1.0f, (f16)0.0625f};
+    const f16x2 kAdd = {(f16)-1032.0f, (f16)-72.0f};
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+        const uint32_t sel = 0x0C000C00u | ((uint32_t)b << 16) | (uint32_t)b;
+        const uint32_t bb = __builtin_amdgcn_perm(w, w, sel);  // [byte b, 0, byte b, 0]
+        const f16x2 q = as_h2((bb & 0x00F0000Fu) ^ 0x64806408u) * kMul + kAdd;
+        out[b] = as_u32(q * s2);
+    }
+}
+
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }

@@ -82,21 +82,6 @@ constexpr int kXPL = kXBytes / 16 / 256;            // X copies per producer lan
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Natural nibble order: byte b of w -> (k_2b, k_2b+1) as exact fp16
-// integers (byte permute, one v_bitop3_b32, one packed fma), times the
-// group scale.
-__device__ __forceinline__ void ws_decode8(uint32_t w, f16x2 s2, uint32_t out[4]) {
-    const f16x2 kMul = {(f16)1.0f, (f16)0.0625f};
-    const f16x2 kAdd = {(f16)-1032.0f, (f16)-72.0f};
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-        const uint32_t sel = 0x0C000C00u | ((uint32_t)b << 16) | (uint32_t)b;
-        const uint32_t bb = __builtin_amdgcn_perm(w, w, sel);  // [byte b, 0, byte b, 0]
-        const f16x2 q = as_h2((bb & 0x00F0000Fu) ^ 0x64806408u) * kMul + kAdd;
-        out[b] = as_u32(q * s2);
-    }
-}
-
 typedef __attribute__((address_space(3))) void* ws_lds_ptr_t;
 // 16 bytes per lane, buffer (rsrc) + per-lane byte offset + wave-uniform
 // byte offset -> LDS wave base + lane * 16 (no VALU address arithmetic).
@@ -227,8 +212,8 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
             uint32_t o[5][4];
             const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) ws_decode8(wd[j], f16x2{sh, sh}, o[j]);
-            ws_decode8(wl, f16x2{shl, shl}, o[4]);
+            for (int j = 0; j < 4; ++j) decode8_natural_scaled(wd[j], f16x2{sh, sh}, o[j]);
+            decode8_natural_scaled(wl, f16x2{shl, shl}, o[4]);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
