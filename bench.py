@@ -22,6 +22,7 @@ reference CPU loop, timed on this host's cores.
     python bench.py --only cfg1 --no-cpu  # one config (profiling runs)
     python bench.py --calib-copy          # plain copy of known size (PMC scale)
     python bench.py --calib-dense-gemm    # hipBLASLt fp16 GEMM at the config 4 shape and two others
+    python bench.py --calib-floor         # launch floor and vendor reads at the suite's byte counts
 """
 from __future__ import annotations
 
@@ -207,6 +208,8 @@ def main():
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 256 MiB device copy 20x (PMC calibration) and exit")
+    ap.add_argument("--calib-floor", action="store_true",
+                    help="graph-replayed launch floor and torch reductions over the suite's byte counts")
     ap.add_argument("--calib-dense-gemm", action="store_true",
                     help="time torch.matmul (hipBLASLt) fp16 X @ W^T at the config 4 shape and exit")
     args = ap.parse_args()
@@ -233,6 +236,41 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log(f"copied {n} bytes x 20")
+        return
+
+    if args.calib_floor:
+        # The fixed cost of a graph-replayed launch (an empty kernel) and the
+        # time of a kernel that only reads B bytes (grid-stride 16-byte loads,
+        # libxinfer_calib.so) at the byte counts of the suite's shapes,
+        # buffers rotated past the Infinity Cache like the projections: what
+        # a projection of the same bytes can reach on this GPU.
+        import ctypes
+        cal = ctypes.CDLL(os.path.join(ROOT, "xinfer_amd", "lib", "libxinfer_calib.so"))
+        cal.xinfer_calib_empty.argtypes = [ctypes.c_void_p]
+        cal.xinfer_calib_read.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                                          ctypes.c_int]
+        sink = torch.zeros(4, dtype=torch.int32, device=dev)
+
+        def empty(i):
+            assert cal.xinfer_calib_empty(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+        w, e = time_launches(torch, empty, 4000, 4000, 1, graph=True)
+        print(json.dumps({"calib": "launch_floor_empty_kernel", "us": round(e * 1e6, 3)}), flush=True)
+        for name, nbytes in (("cfg0_qproj_m1", 6144 * 5120 // 2), ("cfg2_down_m1", 5120 * 17408 // 2),
+                             ("cfg1_gate_up_m1", 2 * 17408 * 5120 // 2),
+                             ("cfg3_lm_head_m1", 151936 * 5120 // 2)):
+            copies = max(1, -(-ROTATE_MIN_BYTES // nbytes))
+            bufs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(copies)]
+            for blocks in (0, 1024):
+                def rd(i, bufs=bufs, nbytes=nbytes, blocks=blocks):
+                    assert cal.xinfer_calib_read(ctypes.c_void_p(torch.cuda.current_stream().cuda_stream),
+                                                 ctypes.c_void_p(bufs[i].data_ptr()), nbytes,
+                                                 ctypes.c_void_p(sink.data_ptr()), blocks) == 0
+                w, e = time_launches(torch, rd, max(copies, 400), max(copies, 400), copies, graph=True)
+                print(json.dumps({"calib": "read_only_kernel", "shape": name, "bytes": nbytes,
+                                  "blocks": blocks or "8 per CU", "us": round(e * 1e6, 3),
+                                  "GBps": round(nbytes / e / 1e9, 1), "frac_hbm": round(nbytes / e / 1e9 / HBM_PEAK_GBPS, 4),
+                                  "copies": copies}), flush=True)
+            del bufs
         return
 
     if args.calib_dense_gemm:

@@ -1,4 +1,5 @@
-"""Build libxinfer_hip.so (gfx950) in-tree with hipcc.
+"""Build libxinfer_hip.so (gfx950) in-tree with hipcc (and bench.py's
+measurement kernels, libxinfer_calib.so).
 
     python -m xinfer_amd.build          # build
     python -m xinfer_amd.build --asm    # also dump gfx950 ISA to _build/
@@ -15,6 +16,9 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT_DIR = os.path.join(HERE, "lib")
 LIB_PATH = os.path.join(OUT_DIR, "libxinfer_hip.so")
+# measurement kernels of bench.py --calib-floor, a library of their own
+CALIB_SRC = os.path.join(HERE, "calib", "read_calib.hip")
+CALIB_LIB = os.path.join(OUT_DIR, "libxinfer_calib.so")
 BUILD_DIR = os.path.join(ROOT, "_build")
 ARCH = "gfx950"
 
@@ -54,6 +58,11 @@ def build(asm: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB_PATH)
+    r = subprocess.run([hipcc(), *HIPCC_FLAGS, "-shared", CALIB_SRC, "-o", CALIB_LIB + ".tmp"],
+                       capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"calibration library failed:\n{r.stderr}")
+    os.replace(CALIB_LIB + ".tmp", CALIB_LIB)
     if asm:
         for src in SOURCES:
             out = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".s")
