@@ -14,7 +14,11 @@
 //     c / (K/32) of the pair, k = 32 (c % (K/32)).  That position is the
 //     same for every pair, so each lane keeps the activations of its P
 //     chunks in registers (permuted to the decode's pair order, with the
-//     chunk's bias term), loaded once: no LDS staging, no barrier.
+//     chunk's bias term), loaded once.  The block stages X once in LDS for
+//     that (one thread per 32-k chunk: 64 bytes loaded, permuted, bias term
+//     summed), and every lane reads its chunks from there: X is fetched
+//     from L2 once per block instead of twice per wave (the two rows of a
+//     pair use the same chunks).
 //   * decode and arithmetic as the GEMV: one v_bitop3_b32 per nibble pair
 //     gives exact biased fp16 integers, v_dot2_f32_f16 into ta / tb, the
 //     chunk's dot product is ta + tb/16 with ta started at the bias term,
@@ -60,6 +64,7 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     constexpr int PF = kPairPF;
     constexpr int K = 1024 * P;
     constexpr int CPR = K / 32;       // 16-byte chunks per row
+    static_assert(CPR <= 256, "one staging thread per chunk");
     constexpr int NG = K / 128;       // scale groups per row
     constexpr uint32_t kRowBytes = K / 2;
 
@@ -74,17 +79,17 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     const int q0 = (int)(gw * p.npairs / nwaves);
     const int q1 = (int)((gw + 1) * p.npairs / nwaves);
 
-    // --- per-lane activations of the lane's P chunks (the same for every
-    // pair): raw loads first; they are permuted after the weight prefetch is
-    // issued (loads complete in order, so that waits for X alone)
-    u32x4 xr[P][4];
+    // --- X staged in LDS once per block: chunk c (32 k, c < K/32) as 64
+    // bytes in the decode's pair order plus its bias term.  The global loads
+    // go out before the weight prefetch (loads complete in issue order, so
+    // the staging then waits for X alone).
+    __shared__ __align__(16) unsigned char xst[CPR * 64];
+    __shared__ float xcb[CPR];
+    u32x4 xr[4];
+    if (tid < CPR) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(p.X + tid * 32);
 #pragma unroll
-    for (int i = 0; i < P; ++i) {
-        const int c = 64 * i + lane;
-        const int cr = c < CPR ? c : c - CPR;
-        const u32x4* src = reinterpret_cast<const u32x4*>(p.X + cr * 32);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) xr[i][v] = src[v];
+        for (int v = 0; v < 4; ++v) xr[v] = src[v];
     }
     f16x2 xp[P][16];  // the chunks' activations in the decode's pair order
     float cb[P];      // chunk bias terms -(1032 sum x_even + 72 sum x_odd)
@@ -179,13 +184,15 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
     __builtin_amdgcn_sched_barrier(0);
 
-#pragma unroll
-    for (int i = 0; i < P; ++i) {
+    if (tid < CPR) {
         float se = 0.0f, so = 0.0f;
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const uint32_t xa[4] = {xr[i][v].x, xr[i][v].y, xr[i][v].z, xr[i][v].w};
-            permute_x8(xa, &xp[i][4 * v]);
+            const uint32_t xa[4] = {xr[v].x, xr[v].y, xr[v].z, xr[v].w};
+            f16x2 pr[4];
+            permute_x8(xa, pr);
+            *reinterpret_cast<u32x4*>(xst + tid * 64 + v * 16) =
+                u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const f16x2 x2 = as_h2(xa[j]);
@@ -193,7 +200,24 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
                 so += (float)x2.y;
             }
         }
-        cb[i] = -(1032.0f * se + 72.0f * so);
+        xcb[tid] = -(1032.0f * se + 72.0f * so);
+    }
+    // LDS writes done, then the barrier; no vmcnt wait (a __syncthreads
+    // release fence would also wait for the weight prefetch in flight)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < P; ++i) {
+        const int c = 64 * i + lane;
+        const int cr = c < CPR ? c : c - CPR;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const u32x4 t = *reinterpret_cast<const u32x4*>(xst + cr * 64 + v * 16);
+            xp[i][4 * v] = as_h2(t.x);
+            xp[i][4 * v + 1] = as_h2(t.y);
+            xp[i][4 * v + 2] = as_h2(t.z);
+            xp[i][4 * v + 3] = as_h2(t.w);
+        }
+        cb[i] = xcb[cr];
     }
 
     // The ring's body has no branch around a load and no global memory
