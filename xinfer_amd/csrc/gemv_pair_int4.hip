@@ -3,12 +3,12 @@
 // Same contract as the decode GEMV (src/ops/linear.cpp:165-305, and the
 // fused descriptors of linear.cpp:351-498) for large decode projections: one
 // activation row, K a multiple of 1024 in 4096..6144, N even, at least 32768
-// rows in the launch.  Two adjacent weight rows are K contiguous bytes, i.e.
-// P = K / 1024 pieces of 1 KB: a wave reads a row pair as P fully coalesced
-// 1 KB loads (lane j takes bytes 16j..16j+15 of each piece).  Streaming whole
-// 1 KB pieces reads faster on MI355X than the GEMV's 512-byte row pieces (a
-// pure read of the north-star matrix: 14.2-14.6 us in pairs against
-// 15.8-17.0 us in the GEMV's pattern).
+// rows in the launch (4096 at K = 6144).  Two adjacent weight rows are K
+// contiguous bytes, i.e. P = K / 1024 pieces of 1 KB: a wave reads a row
+// pair as P fully coalesced 1 KB loads (lane j takes bytes 16j..16j+15 of
+// each piece).  Streaming whole 1 KB pieces reads faster on MI355X than the
+// GEMV's 512-byte row pieces (a pure read of the north-star matrix:
+// 14.2-14.6 us in pairs against 15.8-17.0 us in the GEMV's pattern).
 //
 //   * lane j's 16 bytes of piece i are chunk c = 64 i + j of the pair: row
 //     c / (K/32) of the pair, k = 32 (c % (K/32)).  That position is the
@@ -34,6 +34,8 @@
 //     while the previous one is computed.  The ring runs whole passes; the
 //     last item is computed after it, so no wave waits on a load issued past
 //     its end.
+
+#include <stdlib.h>
 
 #include "common.h"
 
@@ -291,7 +293,16 @@ PairKernel pair_kernel_for(int P) {
 // wins consistently (N = 8192 and 17408 at K = 5120 are 1-6 % faster on the
 // GEMV).
 bool pair_takes(int64_t M, int64_t K, int64_t n_total) {
-    return M == 1 && K % 1024 == 0 && K >= 4096 && K <= 6144 && n_total >= 32768;
+    static const int64_t min_rows = [] {  // XINFER_PAIR_MIN_ROWS: tuning override
+        const char* v = getenv("XINFER_PAIR_MIN_ROWS");
+        return (v && *v) ? (int64_t)atoll(v) : (int64_t)32768;
+    }();
+    // K = 6144 (o_proj): the pair kernel wins from 5120 rows (residual
+    // 6.29 -> 5.94 us, plain + add_inplace 7.57 -> 7.33); at K = 5120 below
+    // 32768 rows the GEMV stays faster (q-proj 5.64 vs 5.73, fused QKV
+    // 8.95 vs 9.2, LA in_proj 10.06 vs 10.3-10.5 us)
+    const int64_t min_here = (K == 6144 && min_rows == 32768) ? 4096 : min_rows;
+    return M == 1 && K % 1024 == 0 && K >= 4096 && K <= 6144 && n_total >= min_here;
 }
 
 // Returns 1 when the launch is left to the GEMV (odd N, shape not taken),
