@@ -27,7 +27,9 @@
 //     those MFMAs run.
 //   * consumer c owns rows 64c .. 64c+63 and the first 128 columns: 2 x 4
 //     tiles of v_mfma_f32_32x32x16_f16 (128 accumulators), plus the last 8
-//     columns as four 16x16x32 tiles whose B operand has 8 live columns.
+//     columns as a third 32-column tile whose B operand has 8 live columns
+//     (it reuses the A operands already in registers: as four 16x16x32
+//     tiles it needed A reads of its own, measured 1.7 % slower).
 //   * LDS layouts are chosen per 16-byte chunk (a copy places any global
 //     16 bytes at any lane slot): each quad of lanes of an X copy reads 64
 //     contiguous bytes of one row, into an XOR-swizzled layout; B is stored
@@ -70,13 +72,14 @@ constexpr int kWStages = 4;
 constexpr int kXBytes = kBM * kStepK * 2;     // 32 KB: blocks of 8 rows x 64 k (1 KB)
 constexpr int kWBytes = kBN * kStepK / 2;     // 4352 B
 constexpr int kBMain = 128 * kStepK * 2;      // 16 KB: [32-col tile][substep] blocks of 1 KB
-constexpr int kBBytes = kBMain + 2 * 1024;    // + the last 8 columns: [k-half] blocks of 1 KB
+constexpr int kBBytes = kBMain + 4 * 1024;    // + the last 8 columns: [substep] blocks of 1 KB
 constexpr int kSChunk = kBN * 16;             // 8 groups of scales per row: 2176 B
 constexpr int kOffX = 0;
 constexpr int kOffW = kOffX + kXStages * kXBytes;   // 98304
 constexpr int kOffB = kOffW + kWStages * kWBytes;   // 115712
-constexpr int kOffS = kOffB + 2 * kBBytes;          // 152576
-constexpr int kLds = kOffS + 2 * kSChunk;           // 156928
+constexpr int kOffS = kOffB + 2 * kBBytes;          // 156672
+constexpr int kLds = kOffS + 2 * kSChunk;           // 161024
+static_assert(kLds <= 160 * 1024, "LDS of one CU");
 constexpr int kXPL = kXBytes / 16 / 256;            // X copies per producer lane per step: 8
 }  // namespace ws
 
@@ -159,8 +162,10 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
         // fp16 bytes each at B block (mn/32, c/2), slot (mn%32) + 32 (c%2)
         // (the 32x32x16 B layout; for a fixed j, 16 consecutive lanes write
         // consecutive slots).  The last 8 rows: dword d = 16 pw + lane
-        // (lanes < 16) = (h, j) = d / 8, row 128 + d % 8 -> block h of the
-        // 16x16x32 part, slot (row - 128) + 16 j.
+        // (lanes < 16) = chunk c = d / 8, row 128 + d % 8 -> block c / 2 of
+        // the last-8 part, slot (row - 128) + 32 (c % 2) (the 32x32x16 B
+        // layout; slots of columns 8-31 are never written: their outputs are
+        // dropped).
         int bdst[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -170,7 +175,7 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
         const int ld = 16 * pw + (lane & 15);
         const int lhj = ld >> 3, lrow = 128 + (ld & 7);
         const int lsrc = 4096 + ((lhj >> 2) * 8 + (ld & 7)) * 16 + (lhj & 3) * 4;
-        const int ldst = kBMain + (lhj >> 2) * 1024 + ((ld & 7) + 16 * (lhj & 3)) * 16;
+        const int ldst = kBMain + (lhj >> 1) * 1024 + ((ld & 7) + 32 * (lhj & 1)) * 16;
         // scales: row r = 64 pw + lane < 136 copies S[r][8c .. 8c+7]
         // (producers 0-2; producer 2 only lanes 0-7)
         const uint32_t soff = (uint32_t)min(n0 + min(64 * pw + lane, kBN - 1), N - 1) * (uint32_t)ng * 2u;
@@ -274,14 +279,15 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int e = 0; e < 16; ++e) acc[mt][j][e] = 0.0f;
-        f32x4 lac[4];  // the last 8 columns, 16-row tiles 4c .. 4c+3
+        f32x16 lac[2];  // the last 8 columns as a 32-column tile (columns 8-31 dead)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) lac[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) lac[mt][e] = 0.0f;
         // X operands (see the copy layout): row r, chunk c sits in block
         // r/8 at slot 4 (8 (c/4) + r%8) + ((c%4) ^ x(r)).  32x32x16 A of
         // 32-row tile mt, substep kk: lane l = row 32 mt + l%32, chunk
-        // 2 kk + l/32 -> xa[mt][kk].  16x16x32 A of 16-row tile 4c + q, k-half
-        // h: lane l = row 16 (4c + q) + l%16, chunk 4 h + l/16 -> lo[q][h].
+        // 2 kk + l/32 -> xa[mt][kk]; the last 8 columns use the same A.
         auto xslot = [](int r, int ch) {
             const int x = ((r >> 2) & 1) | (((r >> 3) & 1) << 1);
             return (r >> 3) * 1024 + 16 * (4 * (8 * (ch >> 2) + (r & 7)) + ((ch & 3) ^ x));
@@ -291,12 +297,7 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
         for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
             for (int kk = 0; kk < 4; ++kk) xa[mt][kk] = xslot(32 * (2 * c + mt) + (lane & 31), 2 * kk + (lane >> 5));
-        int lo[4][2];
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-#pragma unroll
-            for (int h = 0; h < 2; ++h) lo[q][h] = xslot(16 * (4 * c + q) + (lane & 15), 4 * h + (lane >> 4));
-        f16x8 a[2][2], b[2][4], al[4], bl;
+        f16x8 a[2][2], b[2][4], bl[2];
         // operands of substep kk of step s into register set `set`
         auto load = [&](int s, int kk, int set) {
             const unsigned char* xs = smem + kOffX + (s % kXStages) * kXBytes;
@@ -307,13 +308,7 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 b[set][j] = *reinterpret_cast<const f16x8*>(bs + (j * 4 + kk) * 1024 + lane * 16);
-        };
-        auto load_left = [&](int s, int h) {
-            const unsigned char* xs = smem + kOffX + (s % kXStages) * kXBytes;
-            const unsigned char* bs = smem + kOffB + (s & 1) * kBBytes;
-            bl = *reinterpret_cast<const f16x8*>(bs + kBMain + h * 1024 + lane * 16);
-#pragma unroll
-            for (int q = 0; q < 4; ++q) al[q] = *reinterpret_cast<const f16x8*>(xs + lo[q][h]);
+            bl[set] = *reinterpret_cast<const f16x8*>(bs + kBMain + kk * 1024 + lane * 16);
         };
         auto mfma_main = [&](int set) {
 #pragma unroll
@@ -321,17 +316,15 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
                     acc[mt][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[set][mt], b[set][j], acc[mt][j], 0, 0, 0);
-        };
-        auto mfma_left = [&]() {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) lac[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[q], bl, lac[q], 0, 0, 0);
+            for (int mt = 0; mt < 2; ++mt)
+                lac[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[set][mt], bl[set], lac[mt], 0, 0, 0);
         };
         __builtin_amdgcn_s_barrier();  // prologue copies landed
         __builtin_amdgcn_s_barrier();  // B0 ready
         load(0, 0, 0);
-        load_left(0, 0);
         // Per step: substeps 0-3 (operands of kk+1 read while the MFMAs of kk
-        // run), the last 8 columns' k-halves after substeps 0 and 2.  The
+        // run), 10 MFMAs per substep (8 + the last 8 columns' 2).  The
         // barrier follows the issue of the step's last MFMAs: every operand
         // of the step is then in registers, and the first operands of the
         // next step are read while those MFMAs run.
@@ -339,31 +332,26 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
             load(s, 1, 1);
             __builtin_amdgcn_sched_barrier(0);
             mfma_main(0);
-            mfma_left();
             __builtin_amdgcn_sched_barrier(0);
             load(s, 2, 0);
-            load_left(s, 1);
             __builtin_amdgcn_sched_barrier(0);
             mfma_main(1);
             __builtin_amdgcn_sched_barrier(0);
             load(s, 3, 1);
             __builtin_amdgcn_sched_barrier(0);
             mfma_main(0);
-            mfma_left();
             __builtin_amdgcn_sched_barrier(0);
             mfma_main(1);
             __builtin_amdgcn_sched_barrier(0);
             __builtin_amdgcn_s_barrier();
             if (s + 1 < nsteps) {
                 load(s + 1, 0, 0);
-                load_left(s + 1, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
         // ---- epilogue: the block's output tile [256][136] is staged in LDS
         // as fp16.  D layout of the 32x32x16 MFMA: lane l, register e:
-        // column l%32, row 8(e/4) + 4(l/32) + e%4; of the 16x16x32 MFMA:
-        // column l%16, row 4(l/16) + e.
+        // column l%32, row 8(e/4) + 4(l/32) + e%4.
         __builtin_amdgcn_s_barrier();  // E1: the producers' copies have landed, stages free
         f16* T = reinterpret_cast<f16*>(smem);
         {
@@ -381,14 +369,14 @@ __global__ __launch_bounds__(512) void gemm_ws_int4_kernel(const GemmWsParams p)
                     }
             }
         }
-        if ((lane & 15) < 8) {
-            const int col = 128 + (lane & 15);
+        if ((lane & 31) < 8) {
+            const int col = 128 + (lane & 31);
             const float bn = (p.bias && n0 + col < N) ? p.bias[n0 + col] : 0.0f;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    T[(64 * c + 16 * q + 4 * (lane >> 4) + e) * kBN + col] = (f16)(lac[q][e] + bn);
+                for (int e = 0; e < 16; ++e)
+                    T[(64 * c + 32 * mt + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3)) * kBN + col] = (f16)(lac[mt][e] + bn);
         }
     }
     __syncthreads();
