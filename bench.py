@@ -365,7 +365,7 @@ def main():
                      "traffic_source": "profiles/traffic_config1_gate_up_m1.json: committed rocprofv3 --pmc "
                                        "FETCH_SIZE + WRITE_SIZE of this kernel, scaled by a plain copy "
                                        "of known size (not measured in this run)",
-                     "kernel": "xhip::gemv_int4_kernel<MR=1,R=2,EPI_SWIGLU,...,PF=1,NWV=8>",
+                     "kernel": "xhip::gemv_pair_int4_kernel<P=5,f16,SWIGLU> (row pairs; each wave streams its gate pairs, then the same up pairs)",
                      "algorithmic_bytes_per_launch": nbytes,
                      "avg_launch_us": round(ev_step * 1e6, 3),
                      "median_launch_us_9_replays": round(ev_med * 1e6, 3),

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "../../include/xinfer_hip/xinfer_ops.h"
 
@@ -249,5 +250,15 @@ int launch_status();           // XINFER_OK or XINFER_ERR_HIP after a launch
 bool pair_takes(int64_t M, int64_t K, int64_t n_total);
 int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
                 int64_t K, bool residual, int* rc);
+int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
+                const void* Su, int64_t N, int64_t K, int* rc);
+// XINFER_PAIR_SWIGLU=0 keeps the M = 1 gate/up SwiGLU on the GEMV (tuning)
+inline bool swiglu_pair_on() {
+    static const bool on = [] {
+        const char* v = getenv("XINFER_PAIR_SWIGLU");
+        return !(v && *v && atoi(v) == 0);
+    }();
+    return on;
+}
 
 }  // namespace xhip_host

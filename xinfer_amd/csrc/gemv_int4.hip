@@ -1000,6 +1000,10 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
     if (M > 8)
         return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
                              (const uint16_t*)scales_up, nullptr, M, N, K);
+    if (M == 1 && !norm_in_kernel && swiglu_pair_on()) {  // large N: the row-pair kernel
+        int prc = XINFER_OK;
+        if (!pair_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, N, K, &prc)) return prc;
+    }
     GemvParams p = {};
     p.ndesc = 1;
     p.X = reinterpret_cast<const f16*>(X);

@@ -29,6 +29,10 @@
 //     global store or load sits inside the streaming loop: on gfx9 the
 //     vector-memory counter counts both, and one there made the compiler
 //     drain the prefetch ring on every item (measured);
+//   * SwiGLU (SWIGLU = true; d[0] = gate, d[1] = up, N rows each): a wave
+//     owns a pair range of both matrices and streams its gate pairs, then
+//     the same up pairs; the epilogue forms silu(g) * u from its own LDS
+//     results, so gate and up rows never cross waves;
 //   * every load is a buffer load with a constant per-lane offset and a
 //     wave-uniform pair offset; one item (the P pieces of one pair) in flight
 //     while the previous one is computed.  The ring runs whole passes; the
@@ -61,7 +65,7 @@ struct PairParams {
 constexpr int kPairMaxPerWave = 128;  // pairs per wave (LDS results: 1 KB per wave)
 constexpr int kPairPF = 1;            // items in flight while one is computed
 
-template <int P, typename OutT>
+template <int P, typename OutT, bool SWIGLU>
 __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p) {
     constexpr int PF = kPairPF;
     constexpr int K = 1024 * P;
@@ -120,16 +124,23 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
         u32x4 w[P];
         uint32_t s[P];
     };
-    const int nitems = q1 - q0;
+    const int nh = q1 - q0;                     // pairs of this wave (per matrix for SwiGLU)
+    const int nitems = SWIGLU ? 2 * nh : nh;
     // a wave without pairs issues its prefetch against empty resources
     const int live = nitems > 0 ? 1 : 0;
     int lit = 0;  // load cursor (item index within the wave)
     auto load_next = [&](Item& b) {
         const int it = lit < nitems ? lit : (nitems > 0 ? nitems - 1 : 0);  // past the end: repeat
         ++lit;
-        const int q = live ? q0 + it : 0;
-        const int di = (q >= pb1) + (q >= pb2) + (q >= pb3);
-        const int qq = q - pick(di, pbs);  // pair within the descriptor
+        int di, qq;  // descriptor, pair within it
+        if (SWIGLU) {
+            di = it >= nh ? 1 : 0;
+            qq = live ? q0 + it - di * nh : 0;
+        } else {
+            const int q = live ? q0 + it : 0;
+            di = (q >= pb1) + (q >= pb2) + (q >= pb3);
+            qq = q - pick(di, pbs);
+        }
         const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
             (void*)(pick(di, dw) + (size_t)qq * 2 * kRowBytes), (short)0, (int)(2 * kRowBytes) * live, 0x00020000);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -247,6 +258,13 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
 
     // results of this wave's rows, per descriptor (wave-uniform), one lane
     // per row: contiguous stores
+    if (SWIGLU) {  // rows 2 q0 .. 2 q1 - 1: gate results at [0, 2 nh), up at [2 nh, 4 nh)
+        for (int i = lane; i < 2 * nh; i += 64) {
+            const float g = res[wave][i], u = res[wave][2 * nh + i];
+            reinterpret_cast<OutT*>(p.d[0].Y)[2 * q0 + i] = (OutT)(g / (1.0f + expf(-g)) * u);
+        }
+        return;
+    }
     for (int di = 0; di < p.ndesc; ++di) {
         const PairDesc& d = p.d[di];
         const int qb = q0 > d.pair_begin ? q0 : d.pair_begin;
@@ -274,12 +292,12 @@ namespace {
 
 typedef void (*PairKernel)(PairParams);
 
-template <typename OutT>
+template <typename OutT, bool SWIGLU = false>
 PairKernel pair_kernel_for(int P) {
     switch (P) {
-        case 4: return gemv_pair_int4_kernel<4, OutT>;
-        case 5: return gemv_pair_int4_kernel<5, OutT>;
-        case 6: return gemv_pair_int4_kernel<6, OutT>;
+        case 4: return gemv_pair_int4_kernel<4, OutT, SWIGLU>;
+        case 5: return gemv_pair_int4_kernel<5, OutT, SWIGLU>;
+        case 6: return gemv_pair_int4_kernel<6, OutT, SWIGLU>;
         default: return nullptr;
     }
 }
@@ -332,6 +350,28 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
     if (!k) return 1;
     int64_t blocks = num_cus();
     const int64_t need = (p.npairs + 4LL * kPairMaxPerWave - 1) / (4LL * kPairMaxPerWave);
+    if (blocks < need) blocks = need;
+    if (blocks > 65535) return 1;
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    *rc = launch_status();
+    return 0;
+}
+
+// M = 1 gate/up SwiGLU (fp16 Y[N] = silu(gate) * up) on the pair kernel.
+// Returns 1 when left to the GEMV (odd N, shape not taken).
+int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
+                const void* Su, int64_t N, int64_t K, int* rc) {
+    if (N % 2 || !pair_takes(1, K, 2 * N)) return 1;
+    PairParams p = {};
+    p.d[0] = PairDesc{Wg, reinterpret_cast<const uint16_t*>(Sg), nullptr, Y, (int32_t)N, 0, 0};
+    p.d[1] = PairDesc{Wu, reinterpret_cast<const uint16_t*>(Su), nullptr, nullptr, (int32_t)N, 0, 0};
+    p.ndesc = 2;
+    p.npairs = (int32_t)(N / 2);
+    p.X = reinterpret_cast<const f16*>(X);
+    PairKernel k = pair_kernel_for<f16, true>((int)(K / 1024));
+    if (!k) return 1;
+    int64_t blocks = num_cus();
+    const int64_t need = (p.npairs + 4LL * (kPairMaxPerWave / 2) - 1) / (4LL * (kPairMaxPerWave / 2));
     if (blocks < need) blocks = need;
     if (blocks > 65535) return 1;
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
