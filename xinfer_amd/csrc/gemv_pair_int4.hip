@@ -59,6 +59,7 @@ struct PairParams {
     PairDesc d[4];
     int32_t ndesc;
     int32_t npairs;     // pairs over all descriptors
+    int32_t strided;    // 1: wave w takes pairs w, w + waves, ...; 0: a contiguous range
     const f16* X;       // [K]
 };
 
@@ -82,8 +83,17 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     // this wave's pairs
     const int64_t nwaves = (int64_t)gridDim.x * 4;
     const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
-    const int q0 = (int)(gw * p.npairs / nwaves);
-    const int q1 = (int)((gw + 1) * p.npairs / nwaves);
+    // Strided (large launches): the pairs of every wave are spread over the
+    // whole matrix, so the XCDs' uneven memory rates average out instead of
+    // some XCDs' waves finishing their contiguous ranges ~0.8 us after
+    // others (north star 16.2-16.3 -> 16.0 us, config 1 16.0 -> 15.8 us;
+    // with 2-3 pairs per wave, as at o_proj, contiguous ranges measured
+    // faster).  q0 = first pair, qs = step, nh = pairs of the wave.
+    const bool strided = p.strided != 0;
+    const int qs = strided ? (int)nwaves : 1;
+    const int q0 = strided ? (int)gw : (int)(gw * p.npairs / nwaves);
+    const int q1 = strided ? (gw < p.npairs ? (int)(gw + (p.npairs - 1 - gw) / nwaves + 1) : (int)gw)
+                           : (int)((gw + 1) * p.npairs / nwaves);
 
     // --- X staged in LDS once per block: chunk c (32 k, c < K/32) as 64
     // bytes in the decode's pair order plus its bias term.  The global loads
@@ -135,9 +145,9 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
         int di, qq;  // descriptor, pair within it
         if (SWIGLU) {
             di = it >= nh ? 1 : 0;
-            qq = live ? q0 + it - di * nh : 0;
+            qq = live ? q0 + (it - di * nh) * qs : 0;
         } else {
-            const int q = live ? q0 + it : 0;
+            const int q = live ? q0 + it * qs : 0;
             di = (q >= pb1) + (q >= pb2) + (q >= pb3);
             qq = q - pick(di, pbs);
         }
@@ -261,7 +271,23 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     if (SWIGLU) {  // rows 2 q0 .. 2 q1 - 1: gate results at [0, 2 nh), up at [2 nh, 4 nh)
         for (int i = lane; i < 2 * nh; i += 64) {
             const float g = res[wave][i], u = res[wave][2 * nh + i];
-            reinterpret_cast<OutT*>(p.d[0].Y)[2 * q0 + i] = (OutT)(g / (1.0f + expf(-g)) * u);
+            reinterpret_cast<OutT*>(p.d[0].Y)[2 * (q0 + (i >> 1) * qs) + (i & 1)] = (OutT)(g / (1.0f + expf(-g)) * u);
+        }
+        return;
+    }
+    if (strided) {  // one lane per result
+        for (int i = lane; i < 2 * nh; i += 64) {
+            const int q = q0 + (i >> 1) * qs;
+            const int di = (q >= pb1) + (q >= pb2) + (q >= pb3);
+            const PairDesc& d = p.d[di];
+            const int n = 2 * (q - pick(di, pbs)) + (i & 1);
+            float v = res[wave][i];
+            if (d.bias) v += d.bias[n];
+            OutT* y = reinterpret_cast<OutT*>(d.Y) + n;
+            if (d.residual)
+                *y = (OutT)((float)*y + (float)(OutT)v);
+            else
+                *y = (OutT)v;
         }
         return;
     }
@@ -346,6 +372,7 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
     p.ndesc = nd;
     p.npairs = pairs;
     p.X = reinterpret_cast<const f16*>(X);
+    p.strided = pairs >= 8 * 4 * num_cus() ? 1 : 0;
     PairKernel k = y_f32 ? pair_kernel_for<float>((int)(K / 1024)) : pair_kernel_for<f16>((int)(K / 1024));
     if (!k) return 1;
     int64_t blocks = num_cus();
@@ -368,6 +395,7 @@ int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const
     p.ndesc = 2;
     p.npairs = (int32_t)(N / 2);
     p.X = reinterpret_cast<const f16*>(X);
+    p.strided = p.npairs >= 4 * 4 * num_cus() ? 1 : 0;
     PairKernel k = pair_kernel_for<f16, true>((int)(K / 1024));
     if (!k) return 1;
     int64_t blocks = num_cus();
