@@ -23,15 +23,16 @@
 //     gives exact biased fp16 integers, v_dot2_f32_f16 into ta / tb, the
 //     chunk's dot product is ta + tb/16 with ta started at the bias term,
 //     scaled by the fp16 group scale in FP32;
-//   * a wave owns a contiguous range of pairs (over all descriptors), so a
-//     row's sum never leaves its wave: 64-lane reduction per pair into a
-//     small per-wave LDS buffer; the results are stored after the loop.  No
+//   * a wave owns a set of pairs (over all descriptors: a contiguous range,
+//     or for large launches every nwaves-th pair), so a row's sum never
+//     leaves its wave: 64-lane reduction per pair into a small per-wave LDS
+//     buffer; the results are stored after the loop.  No
 //     global store or load sits inside the streaming loop: on gfx9 the
 //     vector-memory counter counts both, and one there made the compiler
 //     drain the prefetch ring on every item (measured);
 //   * SwiGLU (SWIGLU = true; d[0] = gate, d[1] = up, N rows each): a wave
-//     owns a pair range of both matrices and streams its gate pairs, then
-//     the same up pairs; the epilogue forms silu(g) * u from its own LDS
+//     owns the same pairs of both matrices and streams its gate pairs, then
+//     its up pairs; the epilogue forms silu(g) * u from its own LDS
 //     results, so gate and up rows never cross waves;
 //   * every load is a buffer load with a constant per-lane offset and a
 //     wave-uniform pair offset; one item (the P pieces of one pair) in flight
