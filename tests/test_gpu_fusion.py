@@ -158,8 +158,8 @@ def test_rmsnorm_fused_prefill_rows(M):
     print(check_f16_tol(to_np(Y), oracle.swiglu_int4(xn, Wg, Sg, Wu, Su, M, 256, K)))
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 5120, 6144), (1, 5120, 17408), (4, 5120, 17408),
-                                   (8, 333, 1024), (64, 1000, 2048), (512, 2048, 1024)])
+@pytest.mark.parametrize("M,N,K", [(1, 5120, 6144), (1, 5120, 17408), (4, 5120, 17408), (3, 5120, 6144),
+                                   (4, 5120, 6144), (8, 333, 1024), (64, 1000, 2048), (512, 2048, 1024)])
 def test_residual_epilogue_bit_exact(M, N, K):
     """residual += o_proj(X) in one launch gives the bits of o_proj into a
     fp16 buffer followed by add_inplace (forward.cpp:229 / 284-290)."""

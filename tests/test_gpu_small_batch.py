@@ -50,7 +50,8 @@ def _check_f32(y, ref):
 
 
 @pytest.mark.parametrize("M,N,K", [(2, 33, 128), (8, 17, 256), (3, 1000, 1536), (8, 4096, 5120),
-                                   (6, 2000, 9984), (4, 5120, 17408), (7, 4100, 8192)])
+                                   (6, 2000, 9984), (4, 5120, 17408), (7, 4100, 8192),
+                                   (3, 5120, 6144), (4, 5120, 6144), (2, 2048, 4096), (4, 6144, 5120)])
 def test_small_batch_shapes(M, N, K):
     import torch
     ops = _ops()
@@ -107,7 +108,8 @@ def test_small_batch_bias_f32():
         _check_f32(to_np(Y), ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(2, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (5, 640, 17408)])
+@pytest.mark.parametrize("M,N,K", [(2, 17408, 5120), (3, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024),
+                                   (5, 640, 17408), (3, 16384, 4096)])
 def test_small_batch_swiglu(M, N, K):
     import torch
     ops = _ops()

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdlib.h>
+#include <type_traits>
 
 #include "../../include/xinfer_hip/xinfer_ops.h"
 
@@ -90,6 +91,19 @@ __device__ __forceinline__ void decode8_natural_scaled(uint32_t w, f16x2 s2, uin
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
     return __builtin_amdgcn_fdot2(a, b, c, false);
 }
+// dot2 starting a new sum in its own register: the compiler forms the
+// two-operand v_dot2c (destination = accumulator) plus a v_mov of the start
+// value; the three-operand encoding needs no copy.
+__device__ __forceinline__ float dot2_from(f16x2 a, f16x2 b, float c) {
+    float d;
+    asm("v_dot2_f32_f16 %0, %1, %2, %3" : "=v"(d) : "v"(a), "v"(b), "v"(c));
+    return d;
+}
+__device__ __forceinline__ float dot2_from0(f16x2 a, f16x2 b) {
+    float d;
+    asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(d) : "v"(a), "v"(b));
+    return d;
+}
 
 // DPP / swizzle lane exchanges.
 template <int CTRL>
@@ -107,6 +121,53 @@ __device__ __forceinline__ float sum32(float v) {
     v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(
         __builtin_bit_cast(int, v), 0x401F));  // xor 16 within 32 lanes
     return v;
+}
+
+// Adds lane L and lane L xor 32 (gfx950 v_permlane32_swap on two copies:
+// the first ends as [lo, lo], the second as [hi, hi]).  Written as asm:
+// the compiler's builtin returns one register for both halves here.
+__device__ __forceinline__ float add_xor32(float x) {
+    float t = x;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(x), "+v"(t));
+    return x + t;
+}
+// Adds lane L and lane L xor 16 (v_permlane16_swap: odd rows of the first
+// copy trade places with even rows of the second).
+__device__ __forceinline__ float add_xor16(float x) {
+    float t = x;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(x), "+v"(t));
+    return x + t;
+}
+
+// Sums NV values (NV = 1, 2, 4 or 8) each over the 64 lanes in one pass.
+// Halving steps on lane bits 0, 1, 2 pair value 2j with 2j+1: each lane
+// keeps the one its bit selects and adds the one its exchange partner
+// kept for it, so after log2(NV) steps lane L holds a partial of value
+// L mod NV; row rotations and the two swaps finish the sums without LDS.
+// Lane L returns the total of v[L mod NV].
+template <int NV>
+__device__ __forceinline__ float wave_sum_multi(const float (&v)[NV], int lane) {
+    static_assert(NV == 1 || NV == 2 || NV == 4 || NV == 8, "NV must be 1, 2, 4 or 8");
+    float a[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) a[j] = v[j];
+    auto halve = [&](auto ctrl, int n, bool bit) {
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const float keep = bit ? a[2 * j + 1] : a[2 * j];
+            const float send = bit ? a[2 * j] : a[2 * j + 1];
+            a[j] = keep + dpp<decltype(ctrl)::value>(send);
+        }
+    };
+    if constexpr (NV >= 2) halve(std::integral_constant<int, 0xB1>{}, NV, (lane & 1) != 0);
+    if constexpr (NV >= 4) halve(std::integral_constant<int, 0x4E>{}, NV / 2, (lane & 2) != 0);
+    if constexpr (NV >= 8) halve(std::integral_constant<int, 0x124>{}, NV / 4, (lane & 4) != 0);
+    float x = a[0];
+    if constexpr (NV < 2) x += dpp<0xB1>(x);
+    if constexpr (NV < 4) x += dpp<0x4E>(x);
+    if constexpr (NV < 8) x += dpp<0x124>(x);
+    x += dpp<0x128>(x);
+    return add_xor32(add_xor16(x));
 }
 
 // Argmax candidate ordering shared by every argmax kernel: larger value
@@ -252,6 +313,10 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
                 int64_t K, bool residual, int* rc);
 int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
                 const void* Su, int64_t N, int64_t K, int* rc);
+int pairm_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32, int64_t M,
+                 int64_t K, bool residual, int* rc);
+int pairm_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
+                 const void* Su, int64_t M, int64_t N, int64_t K, int* rc);
 // XINFER_PAIR_SWIGLU=0 keeps the M = 1 gate/up SwiGLU on the GEMV (tuning)
 inline bool swiglu_pair_on() {
     static const bool on = [] {

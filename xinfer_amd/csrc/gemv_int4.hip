@@ -865,6 +865,7 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     if (M >= 2 && M <= mb_max_m()) {
         const xinfer_fused_desc one = {Y, W, S, bias, N};
         int mrc = XINFER_OK;
+        if (!pairm_linear(st, &one, 1, X, y_f32, M, K, residual, &mrc)) return mrc;
         if (!mb_linear(st, &one, 1, X, y_f32, M, K, residual, &mrc)) return mrc;
     }
     if (M > 8)
@@ -957,6 +958,7 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
     if (nd == 0) return XINFER_OK;
     if (M >= 2 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
+        if (!pairm_linear(st, live, nd, X, false, M, K, false, &mrc)) return mrc;
         if (!mb_linear(st, live, nd, X, false, M, K, false, &mrc)) return mrc;
     }
     if (M > 8) {  // one GEMM per descriptor
@@ -994,6 +996,7 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
     if ((rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel))) return rc;
     if (M >= 2 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
+        if (!pairm_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc)) return mrc;
         if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc))
             return mrc;
     }

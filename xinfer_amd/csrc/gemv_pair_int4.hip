@@ -1,4 +1,5 @@
-// M = 1 INT4-G128-SYM GEMV streaming weight rows in pairs (gfx950).
+// M = 1 INT4-G128-SYM GEMV streaming weight rows in pairs (gfx950), and
+// its M = 2..4 form (gemv_pairm_int4_kernel, after the M = 1 kernel).
 //
 // Same contract as the decode GEMV (src/ops/linear.cpp:165-305, and the
 // fused descriptors of linear.cpp:351-498) for large decode projections: one
@@ -193,14 +194,9 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     // the pair's two row sums into this wave's LDS buffer
     __shared__ float res[4][2 * kPairMaxPerWave];
     auto finish_pair = [&](int q) {
-        float r[2];
-#pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-            const float v = sum32(acc[rr]);
-            r[rr] = v + __shfl_xor(v, 32);
-            acc[rr] = 0.0f;
-        }
-        if (lane < 2) res[wave][2 * (q - q0) + lane] = lane ? r[1] : r[0];
+        const float r = wave_sum_multi<2>(acc, lane);  // lane 0: row 0, lane 1: row 1
+        acc[0] = acc[1] = 0.0f;
+        if (lane < 2) res[wave][2 * (q - q0) + lane] = r;
     };
 
     Item buf[PF + 1];
@@ -309,6 +305,284 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     }
 }
 
+
+// M = 2..4 activation rows on the row-pair pattern (dot2 per row, no
+// MFMA): the pieces of a pair are split over WPP waves so that a lane's
+// activations (16 fp16 pairs per piece and row) stay in registers; the
+// waves of a pair meet in LDS after the loop.  Same decode, bias terms and
+// per-piece arithmetic as the M = 1 kernel; items, strides and the ring
+// as there, per pair group (WPP waves).  A wave's part H of the pieces is a
+// compile-time constant (one copy of the loop per part, chosen by a
+// wave-uniform branch), so the pieces' rows and the split piece's lane
+// select are known to the compiler as in the M = 1 kernel.
+// waves per pair: as few as keep a wave's activations (16 VGPRs per piece
+// and row) within about 160 VGPRs
+constexpr int pairm_wpp(int P, int MR) { return (MR * P <= 10) ? 1 : (MR * ((P + 1) / 2) <= 12) ? 2 : 4; }
+template <int P, int MR>
+struct PairmShape {
+    static constexpr int WPP = pairm_wpp(P, MR);
+    static constexpr int PA = (P + WPP - 1) / WPP;  // pieces of parts 0.., the last part may have fewer
+    static constexpr int GPB = 4 / WPP;             // pair groups per block
+};
+constexpr int kPairmMaxItems = 64;  // items per pair group (LDS results)
+
+template <int P, int MR, typename OutT, bool SWIGLU>
+__global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p) {
+    constexpr int K = 1024 * P;
+    constexpr int CPR = K / 32;
+    constexpr int NG = K / 128;
+    constexpr uint32_t kRowBytes = K / 2;
+    constexpr int WPP = PairmShape<P, MR>::WPP;
+    constexpr int PA = PairmShape<P, MR>::PA;
+    constexpr int GPB = PairmShape<P, MR>::GPB;
+    constexpr int NV = 2 * MR <= 4 ? 4 : 8;  // sums per item, padded to a power of two
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool hi = lane >= 32;
+    const int hw = wave % WPP;               // part of the pair's pieces
+    const int pg = wave / WPP;               // pair group of the block
+
+    const int64_t ngroups = (int64_t)gridDim.x * GPB;
+    const int64_t gw = (int64_t)blockIdx.x * GPB + pg;
+    const bool strided = p.strided != 0;
+    const int qs = strided ? (int)ngroups : 1;
+    const int q0 = strided ? (int)gw : (int)(gw * p.npairs / ngroups);
+    const int q1 = strided ? (gw < p.npairs ? (int)(gw + (p.npairs - 1 - gw) / ngroups + 1) : (int)gw)
+                           : (int)((gw + 1) * p.npairs / ngroups);
+    const int nh = q1 - q0;
+    const int nitems = SWIGLU ? 2 * nh : nh;
+
+    // X staged once per block: chunk c of row m (32 k) as 64 bytes in the
+    // decode's pair order plus its bias term
+    __shared__ __align__(16) unsigned char xst[MR][CPR * 64];
+    __shared__ float xcb[MR][CPR];
+    // per item: 2 rows x MR sums of each wave (index (2 it + row) MR + m)
+    __shared__ float res[4][kPairmMaxItems * 2 * MR];
+
+    const int nd = p.ndesc;
+    const int pb1 = nd > 1 ? p.d[1].pair_begin : 0x7FFFFFFF;
+    const int pb2 = nd > 2 ? p.d[2].pair_begin : 0x7FFFFFFF;
+    const int pb3 = nd > 3 ? p.d[3].pair_begin : 0x7FFFFFFF;
+    // selects by value (an indexed local array would live in scratch)
+    auto sel = [](int di, auto a0, auto a1, auto a2, auto a3) { return di == 0 ? a0 : di == 1 ? a1 : di == 2 ? a2 : a3; };
+
+    auto body = [&](auto part) {
+        constexpr int H = decltype(part)::value;
+        constexpr int NPC = (P - H * PA) < PA ? (P - H * PA) : PA;  // pieces of this part (>= 1)
+        static_assert(NPC >= 1, "every part has a piece");
+
+        constexpr int kXR = (MR * CPR + 255) / 256;  // staged chunks per thread
+        u32x4 xr[kXR][4];
+#pragma unroll
+        for (int r = 0; r < kXR; ++r) {
+            const int c = tid + 256 * r;
+            if (c < MR * CPR) {
+                const u32x4* src = reinterpret_cast<const u32x4*>(p.X + (size_t)(c / CPR) * K + (c % CPR) * 32);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) xr[r][v] = src[v];
+            }
+        }
+        f16x2 xp[NPC][MR][16];
+        float cb[NPC][MR];
+        uint32_t soff[NPC];
+#pragma unroll
+        for (int i = 0; i < NPC; ++i) {
+            const int c = 64 * (H * PA + i) + lane;
+            const int row = c < CPR ? 0 : 1;
+            const int cr = c - row * CPR;
+            soff[i] = (uint32_t)(row * NG + (cr >> 2)) * 2u;
+        }
+
+        struct Item {
+            u32x4 w[NPC];
+            uint32_t s[NPC];
+        };
+        const int live = nitems > 0 ? 1 : 0;
+        int lit = 0;
+        auto load_next = [&](Item& b) {
+            const int it = lit < nitems ? lit : (nitems > 0 ? nitems - 1 : 0);
+            ++lit;
+            int di, qq;
+            if (SWIGLU) {
+                di = it >= nh ? 1 : 0;
+                qq = live ? q0 + (it - di * nh) * qs : 0;
+            } else {
+                const int q = live ? q0 + it * qs : 0;
+                di = (q >= pb1) + (q >= pb2) + (q >= pb3);
+                qq = q - sel(di, 0, pb1, pb2, pb3);
+            }
+            const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(sel(di, p.d[0].W, p.d[1].W, p.d[2].W, p.d[3].W) + (size_t)qq * 2 * kRowBytes), (short)0,
+                (int)(2 * kRowBytes) * live, 0x00020000);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void*)(sel(di, p.d[0].S, p.d[1].S, p.d[2].S, p.d[3].S) + (size_t)qq * 2 * NG), (short)0,
+                (int)(2 * NG * 2) * live, 0x00020000);
+#pragma unroll
+            for (int i = 0; i < NPC; ++i) {
+                b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (H * PA + i) * 1024 + lane * 16, 0, 2);
+                b.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff[i], 0, 0);
+            }
+        };
+
+        // sums of the pair's row 0 / row 1 per activation row; a piece that
+        // straddles the rows (P odd, the middle one) splits at lane 32
+        float acc[2][MR];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) acc[rr][m] = 0.0f;
+        auto compute_item = [&](const Item& b) {
+#pragma unroll
+            for (int i = 0; i < NPC; ++i) {
+                f16x2 hv[16];
+                decode16_biased(b.w[i].x, b.w[i].y, &hv[0]);
+                decode16_biased(b.w[i].z, b.w[i].w, &hv[8]);
+                const float sc = h2f((uint16_t)b.s[i]);
+                const int pc = H * PA + i;  // constant after unrolling
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    float ta = dot2_from(hv[0], xp[i][m][0], cb[i][m]);
+                    float tb = dot2_from0(hv[1], xp[i][m][1]);
+#pragma unroll
+                    for (int k = 2; k < 16; k += 2) {
+                        ta = dot2(hv[k], xp[i][m][k], ta);
+                        tb = dot2(hv[k + 1], xp[i][m][k + 1], tb);
+                    }
+                    const float v = __builtin_fmaf(tb, 0.0625f, ta) * sc;
+                    if (64 * pc + 63 < CPR) {
+                        acc[0][m] += v;
+                    } else if (64 * pc >= CPR) {
+                        acc[1][m] += v;
+                    } else {
+                        acc[0][m] += hi ? 0.0f : v;
+                        acc[1][m] += hi ? v : 0.0f;
+                    }
+                }
+            }
+        };
+
+        auto finish_item = [&](int it) {
+            float v[NV];
+#pragma unroll
+            for (int j = 0; j < NV; ++j) v[j] = j < 2 * MR ? acc[j / MR][j % MR] : 0.0f;
+            const float r = wave_sum_multi<NV>(v, lane);  // lane j: sum j (pair row j / MR, batch row j % MR)
+#pragma unroll
+            for (int rr = 0; rr < 2; ++rr)
+#pragma unroll
+                for (int m = 0; m < MR; ++m) acc[rr][m] = 0.0f;
+            if (lane < 2 * MR) res[wave][it * 2 * MR + lane] = r;
+        };
+
+        Item buf[2];
+        load_next(buf[0]);
+        __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+        for (int r = 0; r < kXR; ++r) {
+            const int c = tid + 256 * r;
+            if (c < MR * CPR) {
+                float se = 0.0f, so = 0.0f;
+                unsigned char* dst = &xst[c / CPR][(c % CPR) * 64];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const uint32_t xa[4] = {xr[r][v].x, xr[r][v].y, xr[r][v].z, xr[r][v].w};
+                    f16x2 pr[4];
+                    permute_x8(xa, pr);
+                    *reinterpret_cast<u32x4*>(dst + v * 16) =
+                        u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const f16x2 x2 = as_h2(xa[j]);
+                        se += (float)x2.x;
+                        so += (float)x2.y;
+                    }
+                }
+                xcb[c / CPR][c % CPR] = -(1032.0f * se + 72.0f * so);
+            }
+        }
+        // LDS writes done, then the barrier (no vmcnt wait: the weight
+        // prefetch stays in flight)
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+#pragma unroll
+        for (int i = 0; i < NPC; ++i) {
+            const int c = 64 * (H * PA + i) + lane;
+            const int cr = c < CPR ? c : c - CPR;
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const u32x4 t = *reinterpret_cast<const u32x4*>(&xst[m][cr * 64 + v * 16]);
+                    xp[i][m][4 * v] = as_h2(t.x);
+                    xp[i][m][4 * v + 1] = as_h2(t.y);
+                    xp[i][m][4 * v + 2] = as_h2(t.z);
+                    xp[i][m][4 * v + 3] = as_h2(t.w);
+                }
+                cb[i][m] = xcb[m][cr];
+            }
+        }
+
+        int cit = 0;
+        int base = 0;
+        for (; base + 2 <= nitems; base += 2) {
+            load_next(buf[1]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_item(buf[0]);
+            finish_item(cit++);
+            load_next(buf[0]);
+            __builtin_amdgcn_sched_barrier(0);
+            compute_item(buf[1]);
+            finish_item(cit++);
+        }
+        if (base < nitems) {
+            compute_item(buf[0]);
+            finish_item(cit++);
+        }
+    };
+    if (hw == 0) {
+        body(std::integral_constant<int, 0>{});
+    } else if constexpr (WPP >= 2) {
+        if (hw == 1) {
+            body(std::integral_constant<int, 1>{});
+        } else if constexpr (WPP >= 4) {
+            if (hw == 2)
+                body(std::integral_constant<int, 2>{});
+            else
+                body(std::integral_constant<int, 3>{});
+        }
+    }
+
+    // the waves of a pair group add their parts (in wave order) and store
+    __syncthreads();
+    if (hw != 0) return;
+    for (int i = lane; i < 2 * MR * nh; i += 64) {
+        const int q = q0 + (i / (2 * MR)) * qs;           // pair (of the gate matrix for SwiGLU)
+        const int rr = (i / MR) & 1, m = i % MR;
+        const int it = i / (2 * MR);
+        float v = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int w = 0; w < WPP; ++w) {
+            v += res[wave + w][(it * 2 + rr) * MR + m];
+            if (SWIGLU) u += res[wave + w][((nh + it) * 2 + rr) * MR + m];
+        }
+        if (SWIGLU) {
+            const int n = 2 * q + rr;
+            reinterpret_cast<OutT*>(p.d[0].Y)[(size_t)m * p.d[0].N + n] = (OutT)(v / (1.0f + expf(-v)) * u);
+        } else {
+            const int di = (q >= pb1) + (q >= pb2) + (q >= pb3);
+            const PairDesc& d = p.d[di];
+            const int n = 2 * (q - sel(di, 0, pb1, pb2, pb3)) + rr;
+            if (d.bias) v += d.bias[n];
+            OutT* y = reinterpret_cast<OutT*>(d.Y) + (size_t)m * d.N + n;
+            if (d.residual)
+                *y = (OutT)((float)*y + (float)(OutT)v);
+            else
+                *y = (OutT)v;
+        }
+    }
+}
+
 }  // namespace xhip
 
 using namespace xhip;
@@ -406,6 +680,104 @@ int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
     *rc = launch_status();
     return 0;
+}
+
+
+namespace {
+template <int P, int MR>
+constexpr int pairm_wpp() { return (MR * P <= 9) ? 1 : (MR * ((P + 1) / 2) <= 12) ? 2 : 4; }
+
+template <typename OutT, bool SW, int MR>
+PairKernel pairm_for_p(int P) {
+    switch (P) {
+        case 4: return gemv_pairm_int4_kernel<4, MR, OutT, SW>;
+        case 5: return gemv_pairm_int4_kernel<5, MR, OutT, SW>;
+        case 6: return gemv_pairm_int4_kernel<6, MR, OutT, SW>;
+        default: return nullptr;
+    }
+}
+template <typename OutT, bool SW>
+PairKernel pairm_kernel_for(int P, int64_t M) {
+    return M == 2 ? pairm_for_p<OutT, SW, 2>(P) : M == 3 ? pairm_for_p<OutT, SW, 3>(P)
+         : M == 4 ? pairm_for_p<OutT, SW, 4>(P) : nullptr;
+}
+// launch: one block per CU (more when a pair group would exceed its LDS
+// results), strided pairs when every group has at least 4
+int pairm_launch(hipStream_t st, PairKernel k, PairParams& p, int P, int64_t M, bool swiglu, int bpc, int* rc) {
+    if (!k) return 1;
+    const int gpb = 4 / xhip::pairm_wpp(P, (int)M);
+    const int64_t cap = swiglu ? kPairmMaxItems / 2 : kPairmMaxItems;  // pairs per group
+    int64_t blocks = (int64_t)num_cus() * bpc;
+    const int64_t need = (p.npairs + gpb * cap - 1) / (gpb * cap);
+    if (blocks < need) blocks = need;
+    if (blocks > 65535) return 1;
+    p.strided = p.npairs >= 4 * gpb * blocks ? 1 : 0;
+    hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
+    *rc = launch_status();
+    return 0;
+}
+// Blocks per CU for an M = 2..4 launch on the row-pair kernel, 0 where the
+// small-batch MFMA kernel is faster.  Measured on MI355X (graph-replayed,
+// rotated weight copies; pair kernel vs MFMA kernel):
+//   gate/up SwiGLU K = 5120, N = 17408: M = 2 18.4 vs 20.2 us (1 block per
+//     CU), M = 3 21.8 vs 26.4 us (2 per CU), M = 4 29.3 vs 27.0 us;
+//   o_proj K = 6144, N = 5120 (residual): M = 2 7.5 vs 6.6, M = 3 8.8 vs
+//     9.6, M = 4 9.9 vs 10.1 us;
+//   fused QKV K = 5120, N = 14336: M = 2 10.2 vs 10.0, M = 3 12.0 vs 11.3,
+//     M = 4 16.6 vs 11.7 us.
+// The dot2 work grows with M (VALU-bound from M = 2) while the MFMA
+// kernel's barely does.  XINFER_PAIRM=0 keeps every M >= 2 shape on the
+// MFMA kernel (tuning).
+int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
+    static const bool on = [] {
+        const char* v = getenv("XINFER_PAIRM");
+        return !(v && v[0] == '0');
+    }();
+    if (!on || K % 1024 || K < 4096 || K > 6144) return 0;
+    if (swiglu) return rows < 32768 ? 0 : M == 2 ? 1 : M == 3 ? 2 : 0;
+    return (K == 6144 && rows >= 4096 && (M == 3 || M == 4)) ? 1 : 0;
+}
+}  // namespace
+
+// M = 2..4 on the row-pair pattern (dot2 per row); returns 1 when the
+// shape is left to the other kernels.
+int pairm_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32, int64_t M,
+                 int64_t K, bool residual, int* rc) {
+    if (nd < 1 || nd > 4) return 1;
+    int64_t rows = 0;
+    for (int i = 0; i < nd; ++i) {
+        if (descs[i].N % 2) return 1;
+        rows += descs[i].N;
+    }
+    const int bpc = pairm_bpc(M, K, rows, false);
+    if (!bpc) return 1;
+    PairParams p = {};
+    int pairs = 0;
+    for (int i = 0; i < nd; ++i) {
+        p.d[i] = PairDesc{descs[i].W_int4, reinterpret_cast<const uint16_t*>(descs[i].scales), descs[i].bias,
+                          descs[i].Y, (int32_t)descs[i].N, pairs, residual ? 1 : 0};
+        pairs += (int)(descs[i].N / 2);
+    }
+    p.ndesc = nd;
+    p.npairs = pairs;
+    p.X = reinterpret_cast<const f16*>(X);
+    const int P = (int)(K / 1024);
+    PairKernel k = y_f32 ? pairm_kernel_for<float, false>(P, M) : pairm_kernel_for<f16, false>(P, M);
+    return pairm_launch(st, k, p, P, M, false, bpc, rc);
+}
+
+int pairm_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
+                 const void* Su, int64_t M, int64_t N, int64_t K, int* rc) {
+    const int bpc = pairm_bpc(M, K, 2 * N, true);
+    if (N % 2 || !bpc) return 1;
+    PairParams p = {};
+    p.d[0] = PairDesc{Wg, reinterpret_cast<const uint16_t*>(Sg), nullptr, Y, (int32_t)N, 0, 0};
+    p.d[1] = PairDesc{Wu, reinterpret_cast<const uint16_t*>(Su), nullptr, nullptr, (int32_t)N, 0, 0};
+    p.ndesc = 2;
+    p.npairs = (int32_t)(N / 2);
+    p.X = reinterpret_cast<const f16*>(X);
+    const int P = (int)(K / 1024);
+    return pairm_launch(st, pairm_kernel_for<f16, true>(P, M), p, P, M, true, bpc, rc);
 }
 
 }  // namespace xhip_host
