@@ -325,6 +325,7 @@ struct PairmShape {
     static constexpr int GPB = 4 / WPP;             // pair groups per block
 };
 constexpr int kPairmMaxItems = 64;  // items per pair group (LDS results)
+constexpr int kPairmPF = 1;         // items in flight while one is computed
 
 template <int P, int MR, typename OutT, bool SWIGLU>
 __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p) {
@@ -475,8 +476,10 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
             if (lane < 2 * MR) res[wave][it * 2 * MR + lane] = r;
         };
 
-        Item buf[2];
-        load_next(buf[0]);
+        constexpr int PF = kPairmPF;
+        Item buf[PF + 1];
+#pragma unroll
+        for (int j = 0; j < PF; ++j) load_next(buf[j]);
         __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
@@ -523,21 +526,25 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
             }
         }
 
+        // the ring as in the M = 1 kernel: whole passes, then the items
+        // already in registers
         int cit = 0;
         int base = 0;
-        for (; base + 2 <= nitems; base += 2) {
-            load_next(buf[1]);
-            __builtin_amdgcn_sched_barrier(0);
-            compute_item(buf[0]);
-            finish_item(cit++);
-            load_next(buf[0]);
-            __builtin_amdgcn_sched_barrier(0);
-            compute_item(buf[1]);
-            finish_item(cit++);
+        for (; base + PF + 1 <= nitems; base += PF + 1) {
+#pragma unroll
+            for (int j = 0; j <= PF; ++j) {
+                load_next(buf[(j + PF) % (PF + 1)]);
+                __builtin_amdgcn_sched_barrier(0);
+                compute_item(buf[j]);
+                finish_item(cit++);
+            }
         }
-        if (base < nitems) {
-            compute_item(buf[0]);
-            finish_item(cit++);
+#pragma unroll
+        for (int j = 0; j < PF; ++j) {
+            if (base + j < nitems) {
+                compute_item(buf[j]);
+                finish_item(cit++);
+            }
         }
     };
     if (hw == 0) {
@@ -727,13 +734,15 @@ int pairm_launch(hipStream_t st, PairKernel k, PairParams& p, int P, int64_t M, 
 //     M = 4 16.6 vs 11.7 us.
 // The dot2 work grows with M (VALU-bound from M = 2) while the MFMA
 // kernel's barely does.  XINFER_PAIRM=0 keeps every M >= 2 shape on the
-// MFMA kernel (tuning).
+// MFMA kernel, XINFER_PAIRM=<n> (n > 0) sends every shape it can take here
+// with n blocks per CU (tuning).
 int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
-    static const bool on = [] {
+    static const int mode = [] {  // -1: measured routing
         const char* v = getenv("XINFER_PAIRM");
-        return !(v && v[0] == '0');
+        return (v && *v) ? atoi(v) : -1;
     }();
-    if (!on || K % 1024 || K < 4096 || K > 6144) return 0;
+    if (mode == 0 || K % 1024 || K < 4096 || K > 6144) return 0;
+    if (mode > 0) return (M >= 2 && M <= 4) ? mode : 0;
     if (swiglu) return rows < 32768 ? 0 : M == 2 ? 1 : M == 3 ? 2 : 0;
     return (K == 6144 && rows >= 4096 && (M == 3 || M == 4)) ? 1 : 0;
 }
