@@ -63,7 +63,74 @@ struct PairParams {
     int32_t npairs;     // pairs over all descriptors
     int32_t strided;    // 1: wave w takes pairs w, w + waves, ...; 0: a contiguous range
     const f16* X;       // [K]
+    // The launch's G pair owners (waves, or pair groups) split the pairs
+    // without a division in the kernel: npairs = wq G + wr, and
+    // n / G = (n wm) >> (32 + ws) for n < 2^31 (host-computed; G^2 < 2^31).
+    int32_t wq, wr, ws;
+    uint64_t wm;
 };
+
+// The kernel arguments used before and in the streaming loop, read
+// together at the kernel's start: the empty asm needs them all in SGPRs, so
+// the compiler issues every load first and waits once (it otherwise chained
+// three dependent load/wait rounds ahead of the first weight load).
+struct PairArgs {
+    const f16* X;
+    const uint8_t* w0;
+    const uint8_t* w1;
+    const uint8_t* w2;
+    const uint8_t* w3;
+    const uint16_t* s0;
+    const uint16_t* s1;
+    const uint16_t* s2;
+    const uint16_t* s3;
+    int pb1, pb2, pb3;  // first pair of descriptors 1-3 (INT_MAX past ndesc)
+    bool strided;
+    int32_t wq, wr, ws;
+    uint64_t wm;
+};
+__device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
+    PairArgs a;
+    a.X = p.X;
+    a.w0 = p.d[0].W;
+    a.w1 = p.d[1].W;
+    a.w2 = p.d[2].W;
+    a.w3 = p.d[3].W;
+    a.s0 = p.d[0].S;
+    a.s1 = p.d[1].S;
+    a.s2 = p.d[2].S;
+    a.s3 = p.d[3].S;
+    const int nd = p.ndesc, r1 = p.d[1].pair_begin, r2 = p.d[2].pair_begin, r3 = p.d[3].pair_begin;
+    const int st = p.strided;
+    a.wq = p.wq;
+    a.wr = p.wr;
+    a.ws = p.ws;
+    a.wm = p.wm;
+    asm volatile("" ::"s"(a.X), "s"(a.w0), "s"(a.w1), "s"(a.w2), "s"(a.w3), "s"(a.s0), "s"(a.s1), "s"(a.s2),
+                 "s"(a.s3), "s"(nd), "s"(r1), "s"(r2), "s"(r3), "s"(st), "s"(a.wq), "s"(a.wr), "s"(a.ws),
+                 "s"(a.wm));
+    a.pb1 = nd > 1 ? r1 : 0x7FFFFFFF;
+    a.pb2 = nd > 2 ? r2 : 0x7FFFFFFF;
+    a.pb3 = nd > 3 ? r3 : 0x7FFFFFFF;
+    a.strided = st != 0;
+    return a;
+}
+
+// Pair range [q0, q0 + nh) of owner g (step qs = 1), or for strided
+// launches pairs g, g + G, ... (nh of them).  A 64-bit division here took
+// ~0.5 us of the kernel's start before the first load could issue.
+__device__ __forceinline__ void pair_range(const PairArgs& a, uint32_t g, int& q0, int& nh) {
+    const uint32_t wq = (uint32_t)a.wq, wr = (uint32_t)a.wr;
+    if (a.strided) {
+        q0 = (int)g;
+        nh = (int)(wq + (g < wr ? 1u : 0u));
+    } else {
+        auto div = [&](uint32_t n) { return (uint32_t)(((uint64_t)n * a.wm) >> (32 + a.ws)); };
+        const uint32_t b = g * wq + div(g * wr), e = (g + 1) * wq + div((g + 1) * wr);
+        q0 = (int)b;
+        nh = (int)(e - b);
+    }
+}
 
 constexpr int kPairMaxPerWave = 128;  // pairs per wave (LDS results: 1 KB per wave)
 constexpr int kPairPF = 1;            // items in flight while one is computed
@@ -81,21 +148,22 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool hi = lane >= 32;
+    const PairArgs a = pair_args(p);
 
     // this wave's pairs
-    const int64_t nwaves = (int64_t)gridDim.x * 4;
-    const int64_t gw = (int64_t)blockIdx.x * 4 + wave;
+    const int nwaves = (int)gridDim.x * 4;
+    const int gw = (int)blockIdx.x * 4 + wave;
     // Strided (large launches): the pairs of every wave are spread over the
     // whole matrix, so the XCDs' uneven memory rates average out instead of
     // some XCDs' waves finishing their contiguous ranges ~0.8 us after
     // others (north star 16.2-16.3 -> 16.0 us, config 1 16.0 -> 15.8 us;
     // with 2-3 pairs per wave, as at o_proj, contiguous ranges measured
     // faster).  q0 = first pair, qs = step, nh = pairs of the wave.
-    const bool strided = p.strided != 0;
-    const int qs = strided ? (int)nwaves : 1;
-    const int q0 = strided ? (int)gw : (int)(gw * p.npairs / nwaves);
-    const int q1 = strided ? (gw < p.npairs ? (int)(gw + (p.npairs - 1 - gw) / nwaves + 1) : (int)gw)
-                           : (int)((gw + 1) * p.npairs / nwaves);
+    const bool strided = a.strided;
+    const int qs = strided ? nwaves : 1;
+    int q0, nh;  // nh = pairs of the wave (per matrix for SwiGLU)
+    pair_range(a, (uint32_t)gw, q0, nh);
+    const int q1 = q0 + nh;  // contiguous ranges: one past the last pair
 
     // --- X staged in LDS once per block: chunk c (32 k, c < K/32) as 64
     // bytes in the decode's pair order plus its bias term.  The global loads
@@ -105,7 +173,7 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     __shared__ float xcb[CPR];
     u32x4 xr[4];
     if (tid < CPR) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(p.X + tid * 32);
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.X + tid * 32);
 #pragma unroll
         for (int v = 0; v < 4; ++v) xr[v] = src[v];
     }
@@ -124,19 +192,12 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
 
     // --- items (pairs).  The descriptors' fields are read once and selected
     // by wave-uniform compares (no kernel-argument load per item).
-    const int nd = p.ndesc;
-    const int pb1 = nd > 1 ? p.d[1].pair_begin : 0x7FFFFFFF;
-    const int pb2 = nd > 2 ? p.d[2].pair_begin : 0x7FFFFFFF;
-    const int pb3 = nd > 3 ? p.d[3].pair_begin : 0x7FFFFFFF;
-    const uint8_t* const dw[4] = {p.d[0].W, p.d[1].W, p.d[2].W, p.d[3].W};
-    const uint16_t* const ds[4] = {p.d[0].S, p.d[1].S, p.d[2].S, p.d[3].S};
-    const int pbs[4] = {0, pb1, pb2, pb3};
-    auto pick = [](int di, auto const (&a)[4]) { return di == 0 ? a[0] : di == 1 ? a[1] : di == 2 ? a[2] : a[3]; };
+    const int pb1 = a.pb1, pb2 = a.pb2, pb3 = a.pb3;
+    auto sel = [](int di, auto a0, auto a1, auto a2, auto a3) { return di == 0 ? a0 : di == 1 ? a1 : di == 2 ? a2 : a3; };
     struct Item {
         u32x4 w[P];
         uint32_t s[P];
     };
-    const int nh = q1 - q0;                     // pairs of this wave (per matrix for SwiGLU)
     const int nitems = SWIGLU ? 2 * nh : nh;
     // a wave without pairs issues its prefetch against empty resources
     const int live = nitems > 0 ? 1 : 0;
@@ -151,12 +212,12 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
         } else {
             const int q = live ? q0 + it * qs : 0;
             di = (q >= pb1) + (q >= pb2) + (q >= pb3);
-            qq = q - pick(di, pbs);
+            qq = q - sel(di, 0, pb1, pb2, pb3);
         }
         const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(pick(di, dw) + (size_t)qq * 2 * kRowBytes), (short)0, (int)(2 * kRowBytes) * live, 0x00020000);
+            (void*)(sel(di, a.w0, a.w1, a.w2, a.w3) + (size_t)qq * 2 * kRowBytes), (short)0, (int)(2 * kRowBytes) * live, 0x00020000);
         const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-            (void*)(pick(di, ds) + (size_t)qq * 2 * NG), (short)0, (int)(2 * NG * 2) * live, 0x00020000);
+            (void*)(sel(di, a.s0, a.s1, a.s2, a.s3) + (size_t)qq * 2 * NG), (short)0, (int)(2 * NG * 2) * live, 0x00020000);
 #pragma unroll
         for (int i = 0; i < P; ++i) {
             b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (int)(i * 1024 + lane * 16), 0, 2);
@@ -277,7 +338,7 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
             const int q = q0 + (i >> 1) * qs;
             const int di = (q >= pb1) + (q >= pb2) + (q >= pb3);
             const PairDesc& d = p.d[di];
-            const int n = 2 * (q - pick(di, pbs)) + (i & 1);
+            const int n = 2 * (q - sel(di, 0, pb1, pb2, pb3)) + (i & 1);
             float v = res[wave][i];
             if (d.bias) v += d.bias[n];
             OutT* y = reinterpret_cast<OutT*>(d.Y) + n;
@@ -344,15 +405,14 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
     const bool hi = lane >= 32;
     const int hw = wave % WPP;               // part of the pair's pieces
     const int pg = wave / WPP;               // pair group of the block
+    const PairArgs a = pair_args(p);
 
-    const int64_t ngroups = (int64_t)gridDim.x * GPB;
-    const int64_t gw = (int64_t)blockIdx.x * GPB + pg;
-    const bool strided = p.strided != 0;
-    const int qs = strided ? (int)ngroups : 1;
-    const int q0 = strided ? (int)gw : (int)(gw * p.npairs / ngroups);
-    const int q1 = strided ? (gw < p.npairs ? (int)(gw + (p.npairs - 1 - gw) / ngroups + 1) : (int)gw)
-                           : (int)((gw + 1) * p.npairs / ngroups);
-    const int nh = q1 - q0;
+    const int ngroups = (int)gridDim.x * GPB;
+    const int gw = (int)blockIdx.x * GPB + pg;
+    const bool strided = a.strided;
+    const int qs = strided ? ngroups : 1;
+    int q0, nh;
+    pair_range(a, (uint32_t)gw, q0, nh);
     const int nitems = SWIGLU ? 2 * nh : nh;
 
     // X staged once per block: chunk c of row m (32 k) as 64 bytes in the
@@ -362,10 +422,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
     // per item: 2 rows x MR sums of each wave (index (2 it + row) MR + m)
     __shared__ float res[4][kPairmMaxItems * 2 * MR];
 
-    const int nd = p.ndesc;
-    const int pb1 = nd > 1 ? p.d[1].pair_begin : 0x7FFFFFFF;
-    const int pb2 = nd > 2 ? p.d[2].pair_begin : 0x7FFFFFFF;
-    const int pb3 = nd > 3 ? p.d[3].pair_begin : 0x7FFFFFFF;
+    const int pb1 = a.pb1, pb2 = a.pb2, pb3 = a.pb3;
     // selects by value (an indexed local array would live in scratch)
     auto sel = [](int di, auto a0, auto a1, auto a2, auto a3) { return di == 0 ? a0 : di == 1 ? a1 : di == 2 ? a2 : a3; };
 
@@ -380,7 +437,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
         for (int r = 0; r < kXR; ++r) {
             const int c = tid + 256 * r;
             if (c < MR * CPR) {
-                const u32x4* src = reinterpret_cast<const u32x4*>(p.X + (size_t)(c / CPR) * K + (c % CPR) * 32);
+                const u32x4* src = reinterpret_cast<const u32x4*>(a.X + (size_t)(c / CPR) * K + (c % CPR) * 32);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) xr[r][v] = src[v];
             }
@@ -415,10 +472,10 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
                 qq = q - sel(di, 0, pb1, pb2, pb3);
             }
             const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-                (void*)(sel(di, p.d[0].W, p.d[1].W, p.d[2].W, p.d[3].W) + (size_t)qq * 2 * kRowBytes), (short)0,
+                (void*)(sel(di, a.w0, a.w1, a.w2, a.w3) + (size_t)qq * 2 * kRowBytes), (short)0,
                 (int)(2 * kRowBytes) * live, 0x00020000);
             const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                (void*)(sel(di, p.d[0].S, p.d[1].S, p.d[2].S, p.d[3].S) + (size_t)qq * 2 * NG), (short)0,
+                (void*)(sel(di, a.s0, a.s1, a.s2, a.s3) + (size_t)qq * 2 * NG), (short)0,
                 (int)(2 * NG * 2) * live, 0x00020000);
 #pragma unroll
             for (int i = 0; i < NPC; ++i) {
@@ -600,6 +657,20 @@ namespace {
 
 typedef void (*PairKernel)(PairParams);
 
+// The split of p.npairs over G owners (see PairParams); false when G is too
+// large for the kernel's 32-bit products (G^2 >= 2^31).
+bool pair_split(PairParams& p, int64_t G) {
+    if (G < 1 || G * G >= (1LL << 31)) return false;
+    p.wq = (int32_t)(p.npairs / G);
+    p.wr = (int32_t)(p.npairs % G);
+    int sh = 0;
+    while ((1LL << sh) < G) ++sh;
+    p.ws = sh;
+    const uint64_t num = 1ULL << (32 + sh);
+    p.wm = (num + (uint64_t)G - 1) / (uint64_t)G;
+    return true;
+}
+
 template <typename OutT, bool SWIGLU = false>
 PairKernel pair_kernel_for(int P) {
     switch (P) {
@@ -660,7 +731,7 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
     int64_t blocks = num_cus();
     const int64_t need = (p.npairs + 4LL * kPairMaxPerWave - 1) / (4LL * kPairMaxPerWave);
     if (blocks < need) blocks = need;
-    if (blocks > 65535) return 1;
+    if (blocks > 65535 || !pair_split(p, 4 * blocks)) return 1;
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
     *rc = launch_status();
     return 0;
@@ -683,7 +754,7 @@ int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const
     int64_t blocks = num_cus();
     const int64_t need = (p.npairs + 4LL * (kPairMaxPerWave / 2) - 1) / (4LL * (kPairMaxPerWave / 2));
     if (blocks < need) blocks = need;
-    if (blocks > 65535) return 1;
+    if (blocks > 65535 || !pair_split(p, 4 * blocks)) return 1;
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
     *rc = launch_status();
     return 0;
@@ -717,7 +788,7 @@ int pairm_launch(hipStream_t st, PairKernel k, PairParams& p, int P, int64_t M, 
     int64_t blocks = (int64_t)num_cus() * bpc;
     const int64_t need = (p.npairs + gpb * cap - 1) / (gpb * cap);
     if (blocks < need) blocks = need;
-    if (blocks > 65535) return 1;
+    if (blocks > 65535 || !pair_split(p, gpb * blocks)) return 1;
     p.strided = p.npairs >= 4 * gpb * blocks ? 1 : 0;
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
     *rc = launch_status();
