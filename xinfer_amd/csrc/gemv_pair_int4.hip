@@ -132,6 +132,11 @@ __device__ __forceinline__ void pair_range(const PairArgs& a, uint32_t g, int& q
     }
 }
 
+// A 32-k chunk's bias term -(1032 sum x_even + 72 sum x_odd) (the biased
+// decode's 1024 + u and 1024 + 16u forms, u = q + 8) as dot2 of the natural
+// (x_2j, x_2j+1) pairs with this constant: products exact in FP32.
+__device__ constexpr f16x2 kBiasPair = {(f16)-1032.0f, (f16)-72.0f};
+
 constexpr int kPairMaxPerWave = 128;  // pairs per wave (LDS results: 1 KB per wave)
 constexpr int kPairPF = 1;            // items in flight while one is computed
 
@@ -266,7 +271,7 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     __builtin_amdgcn_sched_barrier(0);
 
     if (tid < CPR) {
-        float se = 0.0f, so = 0.0f;
+        float c0 = 0.0f, c1 = 0.0f;  // the bias term as dot2 of (x_even, x_odd) with (-1032, -72)
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
             const uint32_t xa[4] = {xr[v].x, xr[v].y, xr[v].z, xr[v].w};
@@ -274,14 +279,12 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
             permute_x8(xa, pr);
             *reinterpret_cast<u32x4*>(xst + tid * 64 + v * 16) =
                 u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const f16x2 x2 = as_h2(xa[j]);
-                se += (float)x2.x;
-                so += (float)x2.y;
-            }
+            c0 = dot2(as_h2(xa[0]), kBiasPair, c0);
+            c1 = dot2(as_h2(xa[1]), kBiasPair, c1);
+            c0 = dot2(as_h2(xa[2]), kBiasPair, c0);
+            c1 = dot2(as_h2(xa[3]), kBiasPair, c1);
         }
-        xcb[tid] = -(1032.0f * se + 72.0f * so);
+        xcb[tid] = c0 + c1;
     }
     // LDS writes done, then the barrier; no vmcnt wait (a __syncthreads
     // release fence would also wait for the weight prefetch in flight)
@@ -543,7 +546,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
         for (int r = 0; r < kXR; ++r) {
             const int c = tid + 256 * r;
             if (c < MR * CPR) {
-                float se = 0.0f, so = 0.0f;
+                float c0 = 0.0f, c1 = 0.0f;
                 unsigned char* dst = &xst[c / CPR][(c % CPR) * 64];
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
@@ -552,14 +555,12 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
                     permute_x8(xa, pr);
                     *reinterpret_cast<u32x4*>(dst + v * 16) =
                         u32x4{as_u32(pr[0]), as_u32(pr[1]), as_u32(pr[2]), as_u32(pr[3])};
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const f16x2 x2 = as_h2(xa[j]);
-                        se += (float)x2.x;
-                        so += (float)x2.y;
-                    }
+                    c0 = dot2(as_h2(xa[0]), kBiasPair, c0);
+                    c1 = dot2(as_h2(xa[1]), kBiasPair, c1);
+                    c0 = dot2(as_h2(xa[2]), kBiasPair, c0);
+                    c1 = dot2(as_h2(xa[3]), kBiasPair, c1);
                 }
-                xcb[c / CPR][c % CPR] = -(1032.0f * se + 72.0f * so);
+                xcb[c / CPR][c % CPR] = c0 + c1;
             }
         }
         // LDS writes done, then the barrier (no vmcnt wait: the weight
