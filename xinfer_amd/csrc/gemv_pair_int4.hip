@@ -68,6 +68,7 @@ struct PairParams {
     // n / G = (n wm) >> (32 + ws) for n < 2^31 (host-computed; G^2 < 2^31).
     int32_t wq, wr, ws;
     uint64_t wm;
+    int32_t G;          // = gridDim.x times owners per block (gridDim is an argument load of its own)
 };
 
 // The kernel arguments used before and in the streaming loop, read
@@ -88,6 +89,7 @@ struct PairArgs {
     bool strided;
     int32_t wq, wr, ws;
     uint64_t wm;
+    int32_t G;
 };
 __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
     PairArgs a;
@@ -106,9 +108,10 @@ __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
     a.wr = p.wr;
     a.ws = p.ws;
     a.wm = p.wm;
+    a.G = p.G;
     asm volatile("" ::"s"(a.X), "s"(a.w0), "s"(a.w1), "s"(a.w2), "s"(a.w3), "s"(a.s0), "s"(a.s1), "s"(a.s2),
                  "s"(a.s3), "s"(nd), "s"(r1), "s"(r2), "s"(r3), "s"(st), "s"(a.wq), "s"(a.wr), "s"(a.ws),
-                 "s"(a.wm));
+                 "s"(a.wm), "s"(a.G));
     a.pb1 = nd > 1 ? r1 : 0x7FFFFFFF;
     a.pb2 = nd > 2 ? r2 : 0x7FFFFFFF;
     a.pb3 = nd > 3 ? r3 : 0x7FFFFFFF;
@@ -155,8 +158,21 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     const bool hi = lane >= 32;
     const PairArgs a = pair_args(p);
 
+    // --- X staged in LDS once per block: chunk c (32 k, c < K/32) as 64
+    // bytes in the decode's pair order plus its bias term.  The global loads
+    // go out first, before the weight prefetch (loads complete in issue order, so
+    // the staging then waits for X alone).
+    __shared__ __align__(16) unsigned char xst[CPR * 64];
+    __shared__ float xcb[CPR];
+    u32x4 xr[4];
+    if (tid < CPR) {
+        const u32x4* src = reinterpret_cast<const u32x4*>(a.X + tid * 32);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) xr[v] = src[v];
+    }
+
     // this wave's pairs
-    const int nwaves = (int)gridDim.x * 4;
+    const int nwaves = a.G;  // gridDim.x * 4
     const int gw = (int)blockIdx.x * 4 + wave;
     // Strided (large launches): the pairs of every wave are spread over the
     // whole matrix, so the XCDs' uneven memory rates average out instead of
@@ -170,18 +186,6 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     pair_range(a, (uint32_t)gw, q0, nh);
     const int q1 = q0 + nh;  // contiguous ranges: one past the last pair
 
-    // --- X staged in LDS once per block: chunk c (32 k, c < K/32) as 64
-    // bytes in the decode's pair order plus its bias term.  The global loads
-    // go out before the weight prefetch (loads complete in issue order, so
-    // the staging then waits for X alone).
-    __shared__ __align__(16) unsigned char xst[CPR * 64];
-    __shared__ float xcb[CPR];
-    u32x4 xr[4];
-    if (tid < CPR) {
-        const u32x4* src = reinterpret_cast<const u32x4*>(a.X + tid * 32);
-#pragma unroll
-        for (int v = 0; v < 4; ++v) xr[v] = src[v];
-    }
     f16x2 xp[P][16];  // the chunks' activations in the decode's pair order
     float cb[P];      // chunk bias terms -(1032 sum x_even + 72 sum x_odd)
 
@@ -410,7 +414,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
     const int pg = wave / WPP;               // pair group of the block
     const PairArgs a = pair_args(p);
 
-    const int ngroups = (int)gridDim.x * GPB;
+    const int ngroups = a.G;  // gridDim.x * GPB
     const int gw = (int)blockIdx.x * GPB + pg;
     const bool strided = a.strided;
     const int qs = strided ? ngroups : 1;
@@ -669,6 +673,7 @@ bool pair_split(PairParams& p, int64_t G) {
     p.ws = sh;
     const uint64_t num = 1ULL << (32 + sh);
     p.wm = (num + (uint64_t)G - 1) / (uint64_t)G;
+    p.G = (int32_t)G;
     return true;
 }
 
