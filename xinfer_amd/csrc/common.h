@@ -294,6 +294,21 @@ __device__ inline u32x4 rms_apply8(u32x4 v, const float* w, float inv) {
     return u32x4{a[0], a[1], a[2], a[3]};
 }
 
+// The same with the chunk's 8 weights already in registers.
+__device__ inline u32x4 rms_apply8(u32x4 v, float4 w0, float4 w1, float inv) {
+    const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    uint32_t a[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const f16x2 h = as_h2(a[j]);
+        f16x2 o;
+        o.x = (f16)((float)h.x * inv * w[2 * j]);
+        o.y = (f16)((float)h.y * inv * w[2 * j + 1]);
+        a[j] = as_u32(o);
+    }
+    return u32x4{a[0], a[1], a[2], a[3]};
+}
+
 }  // namespace xhip
 
 // Host-side helpers shared by the C-ABI translation units.
@@ -310,9 +325,9 @@ int launch_status();           // XINFER_OK or XINFER_ERR_HIP after a launch
 // GEMV, else 0 with *rc the launch status).
 bool pair_takes(int64_t M, int64_t K, int64_t n_total);
 int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-                int64_t K, bool residual, int* rc);
+                int64_t K, bool residual, const float* norm_w, float eps, int* rc);
 int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
-                const void* Su, int64_t N, int64_t K, int* rc);
+                const void* Su, int64_t N, int64_t K, const float* norm_w, float eps, int* rc);
 int pairm_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32, int64_t M,
                  int64_t K, bool residual, int* rc);
 int pairm_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,

@@ -874,7 +874,7 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     if (M == 1) {  // large N: the row-pair kernel
         const xinfer_fused_desc one = {Y, W, S, bias, N};
         int prc = XINFER_OK;
-        if (!pair_linear(st, &one, 1, X, y_f32, K, residual, &prc)) return prc;
+        if (!pair_linear(st, &one, 1, X, y_f32, K, residual, nullptr, 0.0f, &prc)) return prc;
     }
     GemvParams p = {};
     p.ndesc = 1;
@@ -970,9 +970,10 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
         }
         return XINFER_OK;
     }
-    if (M == 1 && !norm_in_kernel) {  // large N: the row-pair kernel (it has no norm prologue)
+    if (M == 1) {  // large N: the row-pair kernel (the norm, if any, in its X staging)
         int prc = XINFER_OK;
-        if (!pair_linear(st, live, nd, X, false, K, false, &prc)) return prc;
+        if (!pair_linear(st, live, nd, X, false, K, false, norm_in_kernel ? norm_w : nullptr, eps, &prc))
+            return prc;
     }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);
@@ -1003,9 +1004,11 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
     if (M > 8)
         return gemm_int4_f16(st, Y, false, X, W_gate, (const uint16_t*)scales_gate, W_up,
                              (const uint16_t*)scales_up, nullptr, M, N, K);
-    if (M == 1 && !norm_in_kernel && swiglu_pair_on()) {  // large N: the row-pair kernel
+    if (M == 1 && swiglu_pair_on()) {  // large N: the row-pair kernel (the norm, if any, in its X staging)
         int prc = XINFER_OK;
-        if (!pair_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, N, K, &prc)) return prc;
+        if (!pair_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, N, K, norm_in_kernel ? norm_w : nullptr,
+                         eps, &prc))
+            return prc;
     }
     GemvParams p = {};
     p.ndesc = 1;

@@ -3,8 +3,8 @@
 //
 // Same contract as the decode GEMV (src/ops/linear.cpp:165-305, and the
 // fused descriptors of linear.cpp:351-498) for large decode projections: one
-// activation row, K a multiple of 1024 in 4096..6144, N even, at least 32768
-// rows in the launch (4096 at K = 6144).  Two adjacent weight rows are K
+// activation row, K a multiple of 1024 in 4096..6144, N even, at least 4096
+// rows in the launch.  Two adjacent weight rows are K
 // contiguous bytes, i.e. P = K / 1024 pieces of 1 KB: a wave reads a row
 // pair as P fully coalesced 1 KB loads (lane j takes bytes 16j..16j+15 of
 // each piece).  Streaming whole 1 KB pieces reads faster on MI355X than the
@@ -69,6 +69,8 @@ struct PairParams {
     int32_t wq, wr, ws;
     uint64_t wm;
     int32_t G;          // = gridDim.x times owners per block (gridDim is an argument load of its own)
+    const float* norm_w; // M = 1 kernel: RMSNorm weight [K] applied to X while staging, or null
+    float norm_eps;
 };
 
 // The kernel arguments used before and in the streaming loop, read
@@ -90,6 +92,7 @@ struct PairArgs {
     int32_t wq, wr, ws;
     uint64_t wm;
     int32_t G;
+    const float* norm_w;
 };
 __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
     PairArgs a;
@@ -109,9 +112,10 @@ __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
     a.ws = p.ws;
     a.wm = p.wm;
     a.G = p.G;
+    a.norm_w = p.norm_w;
     asm volatile("" ::"s"(a.X), "s"(a.w0), "s"(a.w1), "s"(a.w2), "s"(a.w3), "s"(a.s0), "s"(a.s1), "s"(a.s2),
                  "s"(a.s3), "s"(nd), "s"(r1), "s"(r2), "s"(r3), "s"(st), "s"(a.wq), "s"(a.wr), "s"(a.ws),
-                 "s"(a.wm), "s"(a.G));
+                 "s"(a.wm), "s"(a.G), "s"(a.norm_w));
     a.pb1 = nd > 1 ? r1 : 0x7FFFFFFF;
     a.pb2 = nd > 2 ? r2 : 0x7FFFFFFF;
     a.pb3 = nd > 3 ? r3 : 0x7FFFFFFF;
@@ -165,10 +169,17 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     __shared__ __align__(16) unsigned char xst[CPR * 64];
     __shared__ float xcb[CPR];
     u32x4 xr[4];
+    float4 nwr[8];  // RMSNorm weights of the chunk (norm_w set)
+    const bool norm = a.norm_w != nullptr;
     if (tid < CPR) {
         const u32x4* src = reinterpret_cast<const u32x4*>(a.X + tid * 32);
 #pragma unroll
         for (int v = 0; v < 4; ++v) xr[v] = src[v];
+        if (norm) {
+            const float4* nsrc = reinterpret_cast<const float4*>(a.norm_w + tid * 32);
+#pragma unroll
+            for (int v = 0; v < 8; ++v) nwr[v] = nsrc[v];
+        }
     }
 
     // this wave's pairs
@@ -274,6 +285,23 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
     __builtin_amdgcn_sched_barrier(0);
 
+    // RMSNorm prologue (fused norm + projection entry points): the row's sum
+    // of squares from the staging registers (one chunk per thread, chunk
+    // order within a wave, then the waves in order: the same bits on every
+    // call), x * inv * w rounded to fp16 as the standalone norm does
+    // (src/ops/rmsnorm.cpp:45-78), then staged like a plain X.
+    if (norm) {
+        __shared__ float rms_red[4];
+        float ss[1] = {tid < CPR ? sumsq32(xr) : 0.0f};
+        const float t = wave_sum_multi<1>(ss, lane);
+        if (lane == 0) rms_red[wave] = t;
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        const float inv = 1.0f / sqrtf((((rms_red[0] + rms_red[1]) + rms_red[2]) + rms_red[3]) / (float)K + p.norm_eps);
+        if (tid < CPR) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) xr[v] = rms_apply8(xr[v], nwr[2 * v], nwr[2 * v + 1], inv);
+        }
+    }
     if (tid < CPR) {
         float c0 = 0.0f, c1 = 0.0f;  // the bias term as dot2 of (x_even, x_odd) with (-1032, -72)
 #pragma unroll
@@ -690,22 +718,17 @@ PairKernel pair_kernel_for(int P) {
 }  // namespace
 
 // Whether the pair kernel takes an M = 1 launch of n_total rows: K a
-// multiple of 1024 in 4096..6144 and at least 32768 rows.  Measured against
-// the GEMV on MI355X (graph-replayed, K = 4096 / 5120 / 6144): N = 34816
-// 14.4 / 16.9 / 19.8 us -> 13.9 / 16.3 / 19.6 us; below 32768 rows neither
-// wins consistently (N = 8192 and 17408 at K = 5120 are 1-6 % faster on the
-// GEMV).
+// multiple of 1024 in 4096..6144 and at least 4096 rows.  Measured against
+// the GEMV on MI355X (graph-replayed, rotated weights): config 0 (N = 6144,
+// K = 5120) 5.61 -> 5.15 us, fused QKV (14336 rows) 8.94 -> 8.66 us, fused
+// LA in_proj (16480 rows) 10.06 -> 9.56 us, o_proj (K = 6144) 6.29 -> 5.5
+// us, the north star (K = 5120, N = 34816) 16.9 -> 15.7 us.
 bool pair_takes(int64_t M, int64_t K, int64_t n_total) {
     static const int64_t min_rows = [] {  // XINFER_PAIR_MIN_ROWS: tuning override
         const char* v = getenv("XINFER_PAIR_MIN_ROWS");
-        return (v && *v) ? (int64_t)atoll(v) : (int64_t)32768;
+        return (v && *v) ? (int64_t)atoll(v) : (int64_t)4096;
     }();
-    // K = 6144 (o_proj): the pair kernel wins from 5120 rows (residual
-    // 6.29 -> 5.94 us, plain + add_inplace 7.57 -> 7.33); at K = 5120 below
-    // 32768 rows the GEMV stays faster (q-proj 5.64 vs 5.73, fused QKV
-    // 8.95 vs 9.2, LA in_proj 10.06 vs 10.3-10.5 us)
-    const int64_t min_here = (K == 6144 && min_rows == 32768) ? 4096 : min_rows;
-    return M == 1 && K % 1024 == 0 && K >= 4096 && K <= 6144 && n_total >= min_here;
+    return M == 1 && K % 1024 == 0 && K >= 4096 && K <= 6144 && n_total >= min_rows;
 }
 
 // Returns 1 when the launch is left to the GEMV (odd N, shape not taken),
@@ -713,7 +736,7 @@ bool pair_takes(int64_t M, int64_t K, int64_t n_total) {
 // measured 8-10 % slower), more when a wave would exceed kPairMaxPerWave
 // pairs.
 int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-                int64_t K, bool residual, int* rc) {
+                int64_t K, bool residual, const float* norm_w, float eps, int* rc) {
     if (nd < 1 || nd > 4) return 1;
     int64_t rows = 0;
     for (int i = 0; i < nd; ++i) {
@@ -731,6 +754,8 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
     p.ndesc = nd;
     p.npairs = pairs;
     p.X = reinterpret_cast<const f16*>(X);
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     p.strided = pairs >= 8 * 4 * num_cus() ? 1 : 0;
     PairKernel k = y_f32 ? pair_kernel_for<float>((int)(K / 1024)) : pair_kernel_for<f16>((int)(K / 1024));
     if (!k) return 1;
@@ -746,7 +771,7 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
 // M = 1 gate/up SwiGLU (fp16 Y[N] = silu(gate) * up) on the pair kernel.
 // Returns 1 when left to the GEMV (odd N, shape not taken).
 int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
-                const void* Su, int64_t N, int64_t K, int* rc) {
+                const void* Su, int64_t N, int64_t K, const float* norm_w, float eps, int* rc) {
     if (N % 2 || !pair_takes(1, K, 2 * N)) return 1;
     PairParams p = {};
     p.d[0] = PairDesc{Wg, reinterpret_cast<const uint16_t*>(Sg), nullptr, Y, (int32_t)N, 0, 0};
@@ -754,6 +779,8 @@ int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const
     p.ndesc = 2;
     p.npairs = (int32_t)(N / 2);
     p.X = reinterpret_cast<const f16*>(X);
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     p.strided = p.npairs >= 4 * 4 * num_cus() ? 1 : 0;
     PairKernel k = pair_kernel_for<f16, true>((int)(K / 1024));
     if (!k) return 1;
