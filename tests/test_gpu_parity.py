@@ -266,6 +266,44 @@ def test_pair_kernel_bias_residual_descs():
         print(check_f16_tol(to_np(Y), ref))
 
 
+@pytest.mark.parametrize("N,K", [(4096, 8192), (6144, 24576), (4100, 7168), (5120, 17408)])
+def test_pair_kernel_long_k(N, K):
+    """M = 1 beyond K = 6144: a row pair's 1 KB pieces split over four
+    waves (parts of P / 4 pieces).  fp16 plain, fp32 with bias, fp16
+    residual, and two descriptors in one launch."""
+    import torch
+    ops = _ops()
+    print("case", N, K, flush=True)
+    Xb = synth.activations(40 + K // 1024, 1, K)
+    X = oracle.f16_to_f32(Xb)
+    W, S = synth.packed_weights(41, N, K), synth.scales(41, N, K)
+    dW, dS, dX = to_dev(W), f16_dev(S), f16_dev(Xb)
+    ref = oracle.linear_int4(X, W, S, 1, N, K, nthreads=cpu_threads())
+    Y = _empty((1, N), torch.float16)
+    ops.linear_int4(Y, dX, dW, dS, None, 1, N, K)
+    print(check_f16_tol(to_np(Y), ref))
+    bias = np.linspace(-1, 1, N).astype(np.float32)
+    Yf = _empty((1, N), torch.float32)
+    ops.linear_int4(Yf, dX, dW, dS, to_dev(bias), 1, N, K)
+    assert np.abs(to_np(Yf) - (ref + bias)).max() <= 1e-4 * max(1.0, np.abs(ref).max())
+    r0 = synth.activations(42, 1, N)
+    R = f16_dev(r0)
+    ops.linear_int4_residual(R, dX, dW, dS, None, 1, N, K)
+    print(check_f16_tol(to_np(R), oracle.f16_to_f32(r0).astype(np.float64) + ref))
+    # two descriptors (pair boundaries inside each)
+    Ns = (N // 2 + 2, N // 2 - 2)
+    descs, outs, refs = [], [], []
+    for q, Nq in enumerate(Ns):
+        Wq, Sq = synth.packed_weights(50 + q, Nq, K), synth.scales(50 + q, Nq, K)
+        refs.append(oracle.linear_int4(X, Wq, Sq, 1, Nq, K, nthreads=cpu_threads()))
+        Yq = _empty((1, Nq), torch.float16)
+        outs.append(Yq)
+        descs.append(ops.FusedProjectionDesc(Yq, to_dev(Wq), f16_dev(Sq), None, Nq))
+    ops.linear_int4_fused(dX, descs, 2, 1, K)
+    for Yq, refq in zip(outs, refs):
+        print(check_f16_tol(to_np(Yq), refq))
+
+
 def test_bias_is_added():
     import torch
     ops = _ops()

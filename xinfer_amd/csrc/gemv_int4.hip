@@ -871,10 +871,11 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
     if (M > 8)
         return gemm_int4_f16(st, Y, y_f32, X, W, (const uint16_t*)S, nullptr, nullptr, bias, M, N, K,
                              residual);
-    if (M == 1) {  // large N: the row-pair kernel
+    if (M == 1) {  // large N: the row-pair kernel (its 4-wave form for long K)
         const xinfer_fused_desc one = {Y, W, S, bias, N};
         int prc = XINFER_OK;
         if (!pair_linear(st, &one, 1, X, y_f32, K, residual, nullptr, 0.0f, &prc)) return prc;
+        if (!pairm_linear(st, &one, 1, X, y_f32, 1, K, residual, &prc)) return prc;
     }
     GemvParams p = {};
     p.ndesc = 1;
@@ -974,6 +975,7 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
         int prc = XINFER_OK;
         if (!pair_linear(st, live, nd, X, false, K, false, norm_in_kernel ? norm_w : nullptr, eps, &prc))
             return prc;
+        if (!norm_in_kernel && !pairm_linear(st, live, nd, X, false, 1, K, false, &prc)) return prc;
     }
     p.ndesc = nd;
     return gemv_f16<EPI_PLAIN, f16>(st, p, M);

@@ -412,13 +412,17 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
 // wave-uniform branch), so the pieces' rows and the split piece's lane
 // select are known to the compiler as in the M = 1 kernel.
 // waves per pair: as few as keep a wave's activations (16 VGPRs per piece
-// and row) within about 160 VGPRs
-constexpr int pairm_wpp(int P, int MR) { return (MR * P <= 10) ? 1 : (MR * ((P + 1) / 2) <= 12) ? 2 : 4; }
+// and row) within about 160 VGPRs (MR = 1, long K: at most 6 pieces a wave)
+constexpr int pairm_wpp(int P, int MR) {
+    return MR == 1 ? (P <= 6 ? 1 : (P + 1) / 2 <= 6 ? 2 : 4)
+                   : (MR * P <= 10) ? 1 : (MR * ((P + 1) / 2) <= 12) ? 2 : 4;
+}
 template <int P, int MR>
 struct PairmShape {
     static constexpr int WPP = pairm_wpp(P, MR);
-    static constexpr int PA = (P + WPP - 1) / WPP;  // pieces of parts 0.., the last part may have fewer
-    static constexpr int GPB = 4 / WPP;             // pair groups per block
+    static constexpr int GPB = 4 / WPP;  // pair groups per block
+    // part H of a pair's pieces: [H P / WPP, (H + 1) P / WPP) (sizes differ by at most one)
+    static constexpr int start(int H) { return H * P / WPP; }
 };
 constexpr int kPairmMaxItems = 64;  // items per pair group (LDS results)
 constexpr int kPairmPF = 1;         // items in flight while one is computed
@@ -430,9 +434,8 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
     constexpr int NG = K / 128;
     constexpr uint32_t kRowBytes = K / 2;
     constexpr int WPP = PairmShape<P, MR>::WPP;
-    constexpr int PA = PairmShape<P, MR>::PA;
     constexpr int GPB = PairmShape<P, MR>::GPB;
-    constexpr int NV = 2 * MR <= 4 ? 4 : 8;  // sums per item, padded to a power of two
+    constexpr int NV = 2 * MR <= 2 ? 2 : 2 * MR <= 4 ? 4 : 8;  // sums per item, padded to a power of two
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -463,7 +466,8 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
 
     auto body = [&](auto part) {
         constexpr int H = decltype(part)::value;
-        constexpr int NPC = (P - H * PA) < PA ? (P - H * PA) : PA;  // pieces of this part (>= 1)
+        constexpr int PS = PairmShape<P, MR>::start(H);              // first piece of this part
+        constexpr int NPC = PairmShape<P, MR>::start(H + 1) - PS;  // pieces of this part
         static_assert(NPC >= 1, "every part has a piece");
 
         constexpr int kXR = (MR * CPR + 255) / 256;  // staged chunks per thread
@@ -482,7 +486,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
         uint32_t soff[NPC];
 #pragma unroll
         for (int i = 0; i < NPC; ++i) {
-            const int c = 64 * (H * PA + i) + lane;
+            const int c = 64 * (PS + i) + lane;
             const int row = c < CPR ? 0 : 1;
             const int cr = c - row * CPR;
             soff[i] = (uint32_t)(row * NG + (cr >> 2)) * 2u;
@@ -514,7 +518,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
                 (int)(2 * NG * 2) * live, 0x00020000);
 #pragma unroll
             for (int i = 0; i < NPC; ++i) {
-                b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (H * PA + i) * 1024 + lane * 16, 0, 2);
+                b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(rw, (PS + i) * 1024 + lane * 16, 0, 2);
                 b.s[i] = __builtin_amdgcn_raw_buffer_load_b16(rs, (int)soff[i], 0, 0);
             }
         };
@@ -533,7 +537,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
                 decode16_biased(b.w[i].x, b.w[i].y, &hv[0]);
                 decode16_biased(b.w[i].z, b.w[i].w, &hv[8]);
                 const float sc = h2f((uint16_t)b.s[i]);
-                const int pc = H * PA + i;  // constant after unrolling
+                const int pc = PS + i;  // constant after unrolling
 #pragma unroll
                 for (int m = 0; m < MR; ++m) {
                     float ta = dot2_from(hv[0], xp[i][m][0], cb[i][m]);
@@ -600,7 +604,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
         for (int i = 0; i < NPC; ++i) {
-            const int c = 64 * (H * PA + i) + lane;
+            const int c = 64 * (PS + i) + lane;
             const int cr = c < CPR ? c : c - CPR;
 #pragma unroll
             for (int m = 0; m < MR; ++m) {
@@ -795,9 +799,6 @@ int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const
 
 
 namespace {
-template <int P, int MR>
-constexpr int pairm_wpp() { return (MR * P <= 9) ? 1 : (MR * ((P + 1) / 2) <= 12) ? 2 : 4; }
-
 template <typename OutT, bool SW, int MR>
 PairKernel pairm_for_p(int P) {
     switch (P) {
@@ -807,8 +808,22 @@ PairKernel pairm_for_p(int P) {
         default: return nullptr;
     }
 }
+// M = 1 with K beyond the row-pair kernel's 6144: a pair's pieces over 4
+// waves (K = 7168 .. 24576)
+template <typename OutT, int P>
+PairKernel pairm_long(int p) {
+    if constexpr (P > 24) {
+        return nullptr;
+    } else {
+        return p == P ? gemv_pairm_int4_kernel<P, 1, OutT, false> : pairm_long<OutT, P + 1>(p);
+    }
+}
 template <typename OutT, bool SW>
 PairKernel pairm_kernel_for(int P, int64_t M) {
+    if (M == 1) {
+        if constexpr (SW) return nullptr;
+        else return pairm_long<OutT, 7>(P);
+    }
     return M == 2 ? pairm_for_p<OutT, SW, 2>(P) : M == 3 ? pairm_for_p<OutT, SW, 3>(P)
          : M == 4 ? pairm_for_p<OutT, SW, 4>(P) : nullptr;
 }
@@ -837,7 +852,10 @@ int pairm_launch(hipStream_t st, PairKernel k, PairParams& p, int P, int64_t M, 
 //   fused QKV K = 5120, N = 14336: M = 2 10.2 vs 10.0, M = 3 12.0 vs 11.3,
 //     M = 4 16.6 vs 11.7 us.
 // The dot2 work grows with M (VALU-bound from M = 2) while the MFMA
-// kernel's barely does.  XINFER_PAIRM=0 keeps every M >= 2 shape on the
+// kernel's barely does.  M = 1 with K = 7168 .. 24576 (past the row-pair
+// kernel's K) runs here with a pair's pieces over 4 waves: config 2's down
+// projection (N = 5120, K = 17408) 10.9 us on the GEMV -> 10.4 us at one
+// block per CU, 10.1-10.2 us at two (three: 11.1 us).  XINFER_PAIRM=0 keeps every M >= 2 shape on the
 // MFMA kernel, XINFER_PAIRM=<n> (n > 0) sends every shape it can take here
 // with n blocks per CU (tuning).
 int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
@@ -845,7 +863,10 @@ int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
         const char* v = getenv("XINFER_PAIRM");
         return (v && *v) ? atoi(v) : -1;
     }();
-    if (mode == 0 || K % 1024 || K < 4096 || K > 6144) return 0;
+    if (mode == 0 || K % 1024) return 0;
+    if (M == 1)  // long K (the row-pair kernel takes K <= 6144); two blocks per CU
+        return (!swiglu && K > 6144 && K <= 24576 && rows >= 4096) ? (mode > 0 ? mode : 2) : 0;
+    if (K < 4096 || K > 6144) return 0;
     if (mode > 0) return (M >= 2 && M <= 4) ? mode : 0;
     if (swiglu) return rows < 32768 ? 0 : M == 2 ? 1 : M == 3 ? 2 : 0;
     return (K == 6144 && rows >= 4096 && (M == 3 || M == 4)) ? 1 : 0;
