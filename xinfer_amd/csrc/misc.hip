@@ -129,6 +129,57 @@ __global__ void dequant_int4_kernel(float* out, const uint8_t* W, const uint16_t
 
 // RMSNorm of one token per block (src/ops/rmsnorm.cpp:45-78): FP32 sum of
 // squares, inv = 1 / sqrt(mean + eps), out = fp16(x * inv * w).
+// One pass for rows of up to 8192 (16-byte aligned, H % 8 == 0): each
+// thread loads its chunks of x and of the weights at once and keeps them in
+// registers, so the row is read once and the weights' latency hides behind
+// the reduction (the two-pass kernel below re-reads x after the reduction
+// and only then requests the weights).  Same expression per element
+// (rmsnorm.cpp:78); the row sum in a fixed order: chunks of a thread, the
+// lanes of a wave, the four waves in order.
+__global__ __launch_bounds__(256) void rmsnorm_f16_reg_kernel(f16* out, const f16* in, const float* w,
+                                                              int32_t H, float eps) {
+    constexpr int kCPT = 4;  // chunks per thread
+    __shared__ float red[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c8 = H >> 3;
+    const u32x4* xr = reinterpret_cast<const u32x4*>(in + (size_t)blockIdx.x * H);
+    const float4* wr = reinterpret_cast<const float4*>(w);
+    u32x4* yr = reinterpret_cast<u32x4*>(out + (size_t)blockIdx.x * H);
+    u32x4 v[kCPT];
+    float4 wa[kCPT], wb[kCPT];
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = tid + u * 256;
+        v[u] = u32x4{0u, 0u, 0u, 0u};
+        if (c < c8) {
+            v[u] = xr[c];
+            wa[u] = wr[2 * c];
+            wb[u] = wr[2 * c + 1];
+        }
+    }
+    float ss[1] = {0.0f};
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const uint32_t a[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const f16x2 h = as_h2(a[j]);
+            const float x0 = (float)h.x, x1 = (float)h.y;
+            ss[0] += x0 * x0;
+            ss[0] += x1 * x1;
+        }
+    }
+    const float t = wave_sum_multi<1>(ss, lane);
+    if (lane == 0) red[wave] = t;
+    __syncthreads();
+    const float inv = 1.0f / sqrtf((((red[0] + red[1]) + red[2]) + red[3]) / (float)H + eps);
+#pragma unroll
+    for (int u = 0; u < kCPT; ++u) {
+        const int c = tid + u * 256;
+        if (c < c8) yr[c] = rms_apply8(v[u], wa[u], wb[u], inv);
+    }
+}
+
 __global__ __launch_bounds__(256) void rmsnorm_f16_kernel(f16* out, const f16* in, const float* w,
                                                           int32_t H, float eps) {
     __shared__ float red[8];
@@ -239,8 +290,10 @@ int xinfer_rmsnorm_f16(void* stream, void* out, const void* in, const float* wei
     if (num_tokens <= 0 || hidden_size <= 0) return XINFER_OK;
     if (!out || !in || !weight) return XINFER_ERR_INVALID_ARG;
     if (num_tokens > (1LL << 30) || hidden_size > (1LL << 30)) return XINFER_ERR_UNSUPPORTED;
-    hipLaunchKernelGGL(rmsnorm_f16_kernel, dim3((unsigned)num_tokens), dim3(256), 0,
-                       reinterpret_cast<hipStream_t>(stream), reinterpret_cast<f16*>(out),
+    const bool one_pass = hidden_size % 8 == 0 && hidden_size <= 8192 && xhip_host::aligned(in, 16) &&
+                          xhip_host::aligned(out, 16) && xhip_host::aligned(weight, 16);
+    hipLaunchKernelGGL(one_pass ? rmsnorm_f16_reg_kernel : rmsnorm_f16_kernel, dim3((unsigned)num_tokens),
+                       dim3(256), 0, reinterpret_cast<hipStream_t>(stream), reinterpret_cast<f16*>(out),
                        reinterpret_cast<const f16*>(in), weight, (int32_t)hidden_size, eps);
     return xhip_host::launch_status();
 }
