@@ -441,8 +441,11 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const bool hi = lane >= 32;
-    const int hw = wave % WPP;               // part of the pair's pieces
     const int pg = wave / WPP;               // pair group of the block
+    // part of the pair's pieces; rotated by the block index, so that with
+    // two blocks on a CU the larger parts land on different SIMDs
+    const int hw = (wave + (int)blockIdx.x) % WPP;
+    const int rslot = pg * WPP + hw;         // this wave's LDS results (by part)
     const PairArgs a = pair_args(p);
 
     const int ngroups = a.G;  // gridDim.x * GPB
@@ -569,7 +572,7 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
             for (int rr = 0; rr < 2; ++rr)
 #pragma unroll
                 for (int m = 0; m < MR; ++m) acc[rr][m] = 0.0f;
-            if (lane < 2 * MR) res[wave][it * 2 * MR + lane] = r;
+            if (lane < 2 * MR) res[rslot][it * 2 * MR + lane] = r;
         };
 
         constexpr int PF = kPairmPF;
@@ -664,8 +667,8 @@ __global__ __launch_bounds__(256) void gemv_pairm_int4_kernel(const PairParams p
         float v = 0.0f, u = 0.0f;
 #pragma unroll
         for (int w = 0; w < WPP; ++w) {
-            v += res[wave + w][(it * 2 + rr) * MR + m];
-            if (SWIGLU) u += res[wave + w][((nh + it) * 2 + rr) * MR + m];
+            v += res[rslot + w][(it * 2 + rr) * MR + m];
+            if (SWIGLU) u += res[rslot + w][((nh + it) * 2 + rr) * MR + m];
         }
         if (SWIGLU) {
             const int n = 2 * q + rr;
