@@ -126,7 +126,7 @@ __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
 // Pair range [q0, q0 + nh) of owner g (step qs = 1), or for strided
 // launches pairs g, g + G, ... (nh of them).  A 64-bit division here took
 // ~0.5 us of the kernel's start before the first load could issue.
-__device__ __forceinline__ void pair_range(const PairArgs& a, uint32_t g, int& q0, int& nh) {
+__host__ __device__ __forceinline__ void pair_range(const PairArgs& a, uint32_t g, int& q0, int& nh) {
     const uint32_t wq = (uint32_t)a.wq, wr = (uint32_t)a.wr;
     if (a.strided) {
         q0 = (int)g;
