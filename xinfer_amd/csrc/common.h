@@ -294,16 +294,29 @@ __device__ inline u32x4 rms_apply8(u32x4 v, const float* w, float inv) {
     return u32x4{a[0], a[1], a[2], a[3]};
 }
 
+// fp32(low / high fp16 half of h) * s, rounded once: v_fma_mix with an
+// addend of -0 (x * s + (-0) is x * s for every x, +0 included), one
+// instruction instead of a conversion and a multiply.
+__device__ __forceinline__ float f16lo_mul(uint32_t h, float s) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(s), "s"(-0.0f));
+    return d;
+}
+__device__ __forceinline__ float f16hi_mul(uint32_t h, float s) {
+    float d;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(d) : "v"(h), "v"(s), "s"(-0.0f));
+    return d;
+}
+
 // The same with the chunk's 8 weights already in registers.
 __device__ inline u32x4 rms_apply8(u32x4 v, float4 w0, float4 w1, float inv) {
     const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
     uint32_t a[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const f16x2 h = as_h2(a[j]);
         f16x2 o;
-        o.x = (f16)((float)h.x * inv * w[2 * j]);
-        o.y = (f16)((float)h.y * inv * w[2 * j + 1]);
+        o.x = (f16)(f16lo_mul(a[j], inv) * w[2 * j]);
+        o.y = (f16)(f16hi_mul(a[j], inv) * w[2 * j + 1]);
         a[j] = as_u32(o);
     }
     return u32x4{a[0], a[1], a[2], a[3]};

@@ -292,7 +292,19 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     // (src/ops/rmsnorm.cpp:45-78), then staged like a plain X.
     if (norm) {
         __shared__ float rms_red[4];
-        float ss[1] = {tid < CPR ? sumsq32(xr) : 0.0f};
+        // sum of squares: dot2 of each fp16 pair with itself (exact
+        // products, FP32 sums), two chains
+        float s0 = 0.0f, s1 = 0.0f;
+        if (tid < CPR) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                s0 = dot2(as_h2(xr[v].x), as_h2(xr[v].x), s0);
+                s1 = dot2(as_h2(xr[v].y), as_h2(xr[v].y), s1);
+                s0 = dot2(as_h2(xr[v].z), as_h2(xr[v].z), s0);
+                s1 = dot2(as_h2(xr[v].w), as_h2(xr[v].w), s1);
+            }
+        }
+        float ss[1] = {s0 + s1};
         const float t = wave_sum_multi<1>(ss, lane);
         if (lane == 0) rms_red[wave] = t;
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
