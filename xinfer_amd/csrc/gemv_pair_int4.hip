@@ -414,8 +414,9 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
 }
 
 
-// M = 2..4 activation rows on the row-pair pattern (dot2 per row, no
-// MFMA): the pieces of a pair are split over WPP waves so that a lane's
+// M = 2..4 activation rows, and M = 1 with K past the M = 1 kernel's 6144,
+// on the row-pair pattern (dot2 per row, no MFMA): the pieces of a pair are
+// split over WPP waves so that a lane's
 // activations (16 fp16 pairs per piece and row) stay in registers; the
 // waves of a pair meet in LDS after the loop.  Same decode, bias terms and
 // per-piece arithmetic as the M = 1 kernel; items, strides and the ring
