@@ -223,17 +223,24 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // to 128 KB is one round (K = 17408, M = 8: 92 KB, 5.75 chunks a thread).
     constexpr int kStageUnroll = NW == 4 ? 8 : 4;
     const int chunks = ngs * 4 * M;  // 64-byte chunks: (group, k-quarter, m)
+    // chunk i -> (m, q): a shift and a mask when M is the power-of-two row
+    // stride MR (the decode shapes M = 4, 8, 16), else a division by M
+    static_assert((MR & (MR - 1)) == 0, "MR is a power of two");
+    constexpr int kLogMR = MR == 4 ? 2 : MR == 8 ? 3 : 4;
+    const bool m_full = M == MR;
+    auto chunk_m = [&](int i) { return m_full ? (i & (MR - 1)) : i % M; };
+    auto chunk_q = [&](int i) { return m_full ? (i >> kLogMR) : i / M; };
     auto get = [&](int i, u32x4 (&xv)[4]) {
-        const int m = i % M;
-        const int q = i / M;
+        const int m = chunk_m(i);
+        const int q = chunk_q(i);
         const u32x4* src = reinterpret_cast<const u32x4*>(
             p.X + (size_t)m * K + (size_t)(g0 + (q >> 2)) * 128 + (q & 3) * 32);
 #pragma unroll
         for (int v = 0; v < 4; ++v) xv[v] = src[v];
     };
     auto put = [&](int i, const u32x4 (&xv)[4]) {
-        const int m = i % M;
-        const int q = i / M;
+        const int m = chunk_m(i);
+        const int q = chunk_q(i);
         const int cq = q & 3, gl = q >> 2;
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
