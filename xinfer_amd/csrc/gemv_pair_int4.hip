@@ -3,8 +3,7 @@
 //
 // Same contract as the decode GEMV (src/ops/linear.cpp:165-305, and the
 // fused descriptors of linear.cpp:351-498) for large decode projections: one
-// activation row, K a multiple of 1024 in 4096..6144, N even, at least 4096
-// rows in the launch.  Two adjacent weight rows are K
+// activation row, K a multiple of 1024 in 4096..6144, N even.  Two adjacent weight rows are K
 // contiguous bytes, i.e. P = K / 1024 pieces of 1 KB: a wave reads a row
 // pair as P fully coalesced 1 KB loads (lane j takes bytes 16j..16j+15 of
 // each piece).  Streaming whole 1 KB pieces reads faster on MI355X than the
@@ -738,15 +737,16 @@ PairKernel pair_kernel_for(int P) {
 }  // namespace
 
 // Whether the pair kernel takes an M = 1 launch of n_total rows: K a
-// multiple of 1024 in 4096..6144 and at least 4096 rows.  Measured against
-// the GEMV on MI355X (graph-replayed, rotated weights): config 0 (N = 6144,
-// K = 5120) 5.61 -> 5.15 us, fused QKV (14336 rows) 8.94 -> 8.66 us, fused
-// LA in_proj (16480 rows) 10.06 -> 9.56 us, o_proj (K = 6144) 6.29 -> 5.5
-// us, the north star (K = 5120, N = 34816) 16.9 -> 15.7 us.
+// multiple of 1024 in 4096..6144 (every descriptor's N even, checked by the
+// callers).  Measured against the GEMV on MI355X (graph-replayed, rotated
+// weights), it is faster at every size: N = 48 / 1024 / 4096 at K = 5120
+// 3.34 / 3.57 / 5.01 -> 3.05 / 3.35 / 4.35 us (K = 4096: 3.36 / 3.57 / 4.51
+// -> 2.57 / 2.91 / 3.73), config 0 (N = 6144) 5.61 -> 5.15 us, fused QKV
+// 8.94 -> 8.66 us, the north star 16.9 -> 15.7 us.
 bool pair_takes(int64_t M, int64_t K, int64_t n_total) {
-    static const int64_t min_rows = [] {  // XINFER_PAIR_MIN_ROWS: tuning override
+    static const int64_t min_rows = [] {  // XINFER_PAIR_MIN_ROWS: fewest rows (tuning override)
         const char* v = getenv("XINFER_PAIR_MIN_ROWS");
-        return (v && *v) ? (int64_t)atoll(v) : (int64_t)4096;
+        return (v && *v) ? (int64_t)atoll(v) : (int64_t)2;
     }();
     return M == 1 && K % 1024 == 0 && K >= 4096 && K <= 6144 && n_total >= min_rows;
 }
