@@ -866,7 +866,11 @@ int pairm_launch(hipStream_t st, PairKernel k, PairParams& p, int P, int64_t M, 
 //   o_proj K = 6144, N = 5120 (residual): M = 2 7.5 vs 6.6, M = 3 8.8 vs
 //     9.6, M = 4 9.9 vs 10.1 us;
 //   fused QKV K = 5120, N = 14336: M = 2 10.2 vs 10.0, M = 3 12.0 vs 11.3,
-//     M = 4 16.6 vs 11.7 us.
+//     M = 4 16.6 vs 11.7 us;
+//   one projection, K = 5120, N = 48 / 1024 / 4096 / 6144 / 8192: M = 3
+//     4.3 / 4.8 / 7.0 / 8.3 / 9.9 vs 7.8 / 8.1 / 8.8 / 8.8 / 9.1 us, M = 4
+//     5.1 / 5.7 / 8.3 / 9.9 / 11.5 vs 7.6 / 8.0 / 8.8 / 8.8 / 9.2 us (M = 2:
+//     within a few percent of the GEMV either way).
 // The dot2 work grows with M (VALU-bound from M = 2) while the MFMA
 // kernel's barely does.  M = 1 with K = 7168 .. 24576 (past the row-pair
 // kernel's K) runs here with a pair's pieces over 4 waves: config 2's down
@@ -884,8 +888,12 @@ int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
         return (!swiglu && K > 6144 && K <= 24576 && rows >= 4096) ? (mode > 0 ? mode : 2) : 0;
     if (K < 4096 || K > 6144) return 0;
     if (mode > 0) return (M >= 2 && M <= 4) ? mode : 0;
+    // short launches at M = 3-4: the MFMA kernel's fixed costs (X slice
+    // staging, planner minimum of one tile range per CU) dominate there
+    if (M == 3 && rows <= 6144) return 1;
+    if (M == 4 && rows <= (K >= 6144 ? 5120 : 4096)) return 1;
     if (swiglu) return rows < 32768 ? 0 : M == 2 ? 1 : M == 3 ? 2 : 0;
-    return (K == 6144 && rows >= 4096 && (M == 3 || M == 4)) ? 1 : 0;
+    return 0;
 }
 }  // namespace
 
