@@ -884,8 +884,10 @@ int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
         return (v && *v) ? atoi(v) : -1;
     }();
     if (mode == 0 || K % 1024) return 0;
-    if (M == 1)  // long K (the row-pair kernel takes K <= 6144); two blocks per CU
-        return (!swiglu && K > 6144 && K <= 24576 && rows >= 4096) ? (mode > 0 ? mode : 2) : 0;
+    // long K at M = 1 (the row-pair kernel takes K <= 6144), two blocks per
+    // CU, from 3072 rows (K = 8192 / 17408: N = 1024 3.6 / 5.4 us on the
+    // GEMV vs 4.2 / 5.7 here, N = 4096 5.8 / 9.4 vs 5.3 / 9.2)
+    if (M == 1) return (!swiglu && K > 6144 && K <= 24576 && rows >= 3072) ? (mode > 0 ? mode : 2) : 0;
     if (K < 4096 || K > 6144) return 0;
     if (mode > 0) return (M >= 2 && M <= 4) ? mode : 0;
     // short launches at M = 3-4: the MFMA kernel's fixed costs (X slice
