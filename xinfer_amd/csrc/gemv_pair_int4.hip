@@ -776,7 +776,7 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
     p.X = reinterpret_cast<const f16*>(X);
     p.norm_w = norm_w;
     p.norm_eps = eps;
-    p.strided = pairs >= 8 * 4 * num_cus() ? 1 : 0;
+    p.strided = pairs >= 4 * 4 * num_cus() ? 1 : 0;  // >= 4 pairs a wave (fused QKV, 7 a wave: 8.62 -> 8.43 us)
     PairKernel k = y_f32 ? pair_kernel_for<float>((int)(K / 1024)) : pair_kernel_for<f16>((int)(K / 1024));
     if (!k) return 1;
     int64_t blocks = num_cus();
