@@ -426,7 +426,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         rigs = [Rig(torch, dev, N, K, 0.02, seed=i) for i, N in enumerate(Ns)]
         copies = min(r.copies for r in rigs)
         nw = torch.linspace(0.5, 1.5, K, dtype=torch.float32, device=dev)
-        for M in (1, 4):
+        for M in (1, 4, 8):
             X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
             Xn = torch.empty_like(X)
             ws = torch.empty(max(1, M * K * 2), dtype=torch.uint8, device=dev)
@@ -445,6 +445,28 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
             record(f"rmsnorm_qkv_m{M}_k5120", {"M": M, "N": list(Ns), "K": K, "us_fused": round(ef * 1e6, 3),
                                                "us_separate": round(es * 1e6, 3)})
         del rigs
+        N, K = 17408, 5120                     # gate/up SwiGLU with the input norm
+        rig = Rig(torch, dev, 2 * N, K, 0.02)
+        for M in (4, 8):
+            X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
+            Xn = torch.empty_like(X)
+            ws = torch.empty(M * K * 2, dtype=torch.uint8, device=dev)
+            Y = torch.empty((M, N), dtype=torch.float16, device=dev)
+
+            def fused_g(i, X=X, Y=Y, M=M, ws=ws):
+                W, S = rig.W[i], rig.S[i]
+                ops.rmsnorm_mlp_gate_up_swiglu_int4(Y, X, nw, 1e-6, W[:N], S[:N], W[N:], S[N:], M, N, K,
+                                                    workspace=ws)
+
+            def separate_g(i, X=X, Xn=Xn, Y=Y, M=M):
+                ops.rmsnorm(Xn, X, nw, M, K, 1e-6)
+                W, S = rig.W[i], rig.S[i]
+                ops.mlp_gate_up_swiglu_int4(Y, Xn, W[:N], S[:N], W[N:], S[N:], M, N, K)
+            _, ef = time_launches(torch, fused_g, steps, warm, rig.copies, graph=graph)
+            _, es = time_launches(torch, separate_g, steps, warm, rig.copies, graph=graph)
+            record(f"rmsnorm_gate_up_m{M}_n17408_k5120", {"M": M, "N": N, "K": K, "us_fused": round(ef * 1e6, 3),
+                                                         "us_separate": round(es * 1e6, 3)})
+        del rig
         N, K = 5120, 6144                      # o_proj of a full-attention layer
         rig = Rig(torch, dev, N, K, 0.02)
         for M in (1, 4):

@@ -834,11 +834,13 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
 // the MFMA small-batch kernel for 2 <= M <= 8 (gemv_mb_int4.hip; each returns
 // 1 when the shape is left to the VALU GEMV here).
 namespace xhip_host {
+// norm_w: RMSNorm of X inside the kernel (M = 4 or 8 with every row whole
+// in one block; otherwise the shape is declined)
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-              int64_t M, int64_t K, bool residual, int* rc);
+              int64_t M, int64_t K, bool residual, int* rc, const float* norm_w = nullptr, float eps = 0.0f);
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
               const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
-              int* rc);
+              int* rc, const float* norm_w = nullptr, float eps = 0.0f);
 int mb_argmax_plan(int64_t M, int64_t N, int64_t K, int* nparts);
 int mb_max_m();  // largest M the small-batch kernel takes (then the GEMM)
 int mb_argmax(hipStream_t st, float* logits, const void* X, const uint8_t* W, const void* S,
@@ -899,6 +901,16 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
 // Returns the X the projection reads and whether the kernel applies the norm.
 bool norm_in_projection(int64_t M, int64_t K) { return M == 1 && xhip_host::gemv_stages_x(1, K); }
 
+// The caller's workspace for the normalised rows, checked wherever the
+// workspace size is non-zero (also when the kernel then applies the norm
+// itself, so that a call's errors do not depend on the route it takes).
+int check_norm_ws(const float* norm_w, int64_t M, int64_t K, const void* ws, size_t ws_bytes) {
+    if (!norm_w || norm_in_projection(M, K)) return XINFER_OK;
+    if (!ws || ws_bytes < (size_t)M * (size_t)K * 2) return XINFER_ERR_SCRATCH;
+    if (!xhip_host::aligned(ws, 16)) return XINFER_ERR_MISALIGNED;
+    return XINFER_OK;
+}
+
 int norm_input(hipStream_t st, const void* X, const float* norm_w, float eps, int64_t M, int64_t K,
                void* ws, size_t ws_bytes, const void** Xp, bool* in_kernel) {
     *Xp = X;
@@ -908,8 +920,7 @@ int norm_input(hipStream_t st, const void* X, const float* norm_w, float eps, in
         *in_kernel = true;
         return XINFER_OK;
     }
-    if (!ws || ws_bytes < (size_t)M * (size_t)K * 2) return XINFER_ERR_SCRATCH;
-    if (!xhip_host::aligned(ws, 16)) return XINFER_ERR_MISALIGNED;
+    if (int rc = check_norm_ws(norm_w, M, K, ws, ws_bytes)) return rc;
     *Xp = ws;
     return xinfer_rmsnorm_f16(st, ws, X, norm_w, M, K, eps);
 }
@@ -930,14 +941,8 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
         int rc = check_common(M, q.N, K, group_size);
         if (rc) return rc;
     }
-    const void* X = X0;
-    bool norm_in_kernel = false;
-    if (int rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel)) return rc;
     GemvParams p = {};
-    p.X = reinterpret_cast<const f16*>(X);
     p.K = (int32_t)K;
-    p.norm_w = norm_in_kernel ? norm_w : nullptr;
-    p.norm_eps = eps;
     xinfer_fused_desc live[4];
     int nd = 0;
     for (int i = 0; i < num_descs; ++i) {
@@ -957,6 +962,22 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
         g.N = (int32_t)q.N;
     }
     if (nd == 0) return XINFER_OK;
+    if (int rc = check_norm_ws(norm_w, M, K, ws, ws_bytes)) return rc;
+    // M = 4 / 8 on the small-batch kernel: the norm in its X staging (no
+    // standalone norm launch) when it takes the shape whole
+    if (norm_w && (M == 4 || M == 8) && M <= mb_max_m()) {
+        int64_t rows = 0;
+        for (int i = 0; i < nd; ++i) rows += live[i].N;
+        int mrc = XINFER_OK;
+        if (!pairm_takes(M, K, rows, false) && !mb_linear(st, live, nd, X0, false, M, K, false, &mrc, norm_w, eps))
+            return mrc;
+    }
+    const void* X = X0;
+    bool norm_in_kernel = false;
+    if (int rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel)) return rc;
+    p.X = reinterpret_cast<const f16*>(X);
+    p.norm_w = norm_in_kernel ? norm_w : nullptr;
+    p.norm_eps = eps;
     if (M >= 2 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
         if (!pairm_linear(st, live, nd, X, false, M, K, false, &mrc)) return mrc;
@@ -994,6 +1015,11 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
         !aligned(scales_gate, 2) || !aligned(scales_up, 2) || !aligned(norm_w, 4))
         return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if ((rc = check_norm_ws(norm_w, M, K, ws, ws_bytes))) return rc;
+    if (norm_w && (M == 4 || M == 8) && M <= mb_max_m() && !pairm_takes(M, K, 2 * N, true)) {
+        int mrc = XINFER_OK;  // the norm in the small-batch kernel's X staging
+        if (!mb_swiglu(st, Y, X0, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc, norm_w, eps)) return mrc;
+    }
     const void* X = X0;
     bool norm_in_kernel = false;
     if ((rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel))) return rc;

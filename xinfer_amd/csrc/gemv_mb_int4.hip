@@ -77,6 +77,8 @@ struct MbParams {
     int32_t tiles_blk;   // 16-row tiles of the largest range
     int32_t nranges;     // tile ranges over all descriptors
     int32_t lkw;         // log2 of the waves that share a run of tiles, splitting its groups
+    const float* norm_w; // RMSNorm weight [K] applied to X while staging (M == MR, one k-slice), or null
+    float norm_eps;
 };
 
 constexpr uint32_t kOutOfRange = 0xFFFFF000u;  // >= every buffer resource size used here
@@ -112,7 +114,7 @@ __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
     return r;
 }
 
-template <int MR, int EPI, typename OutT, int NW>
+template <int MR, int EPI, typename OutT, int NW, bool NORM = false>
 __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p) {
     constexpr int E = (EPI == MB_SWIGLU) ? 2 : 1;  // sums per output (weight tiles per item)
     constexpr int NT = 64 * NW;
@@ -158,6 +160,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     float* candv = outl + ((size_t)p.tiles_blk * 16 * M * E << p.lkw);
     int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
     int32_t* flag = candi + NW;
+    // RMSNorm (norm_w set): the weights [K] and the waves' row sums [NW][MR]
+    float* nws = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(candv) + 2 * NW * 4 + 16);
+    float* rsum = nws + K;
 
     // Waves come in runs of kw = 2^lkw: the waves of a run share its tiles
     // and split the slice's groups evenly (every wave gets at least one
@@ -254,15 +259,70 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u)
         if (tid + u * NT < chunks) get(tid + u * NT, xv0[u]);
+    // RMSNorm weights: requested with X, stored to LDS once they land (the
+    // host keeps K <= 6144: K / 4 <= kNormPT * NT)
+    constexpr bool norm = NORM;  // p.norm_w set
+    constexpr int kNormPT = 1536 / NT;
+    float4 nwv[kNormPT];
+#pragma unroll
+    for (int u = 0; u < kNormPT; ++u) nwv[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (norm) {
+#pragma unroll
+        for (int u = 0; u < kNormPT; ++u)
+            nwv[u] = reinterpret_cast<const float4*>(p.norm_w)[min(tid + u * NT, (K >> 2) - 1)];
+    }
 
     constexpr int PF = XHIP_MB_PF;  // items in flight per wave
     MbItem<E> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
 
+    // RMSNorm prologue (fused norm + projection entry points; the host
+    // plans one k-slice, M == MR and one staging round, so a thread's
+    // chunks are all of row tid % MR and the block holds every row whole):
+    // the row's sum of squares in a fixed order (a thread's chunks, the
+    // lanes of the row in xor order, the waves in order), then x * inv * w
+    // rounded to fp16 per element as the standalone norm does
+    // (src/ops/rmsnorm.cpp:45-78).
+    float inv = 0.0f;
+    if constexpr (norm) {
+#pragma unroll
+        for (int u = 0; u < kNormPT; ++u)
+            if (tid + u * NT < (K >> 2)) reinterpret_cast<float4*>(nws)[tid + u * NT] = nwv[u];
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u)
+            if (tid + u * NT < chunks) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    s0 = dot2(as_h2(xv0[u][t].x), as_h2(xv0[u][t].x), s0);
+                    s1 = dot2(as_h2(xv0[u][t].y), as_h2(xv0[u][t].y), s1);
+                    s0 = dot2(as_h2(xv0[u][t].z), as_h2(xv0[u][t].z), s0);
+                    s1 = dot2(as_h2(xv0[u][t].w), as_h2(xv0[u][t].w), s1);
+                }
+            }
+        float sr = s0 + s1;
+#pragma unroll
+        for (int off = MR; off < 64; off <<= 1) sr += __shfl_xor(sr, off);
+        if (lane < MR) rsum[wave * MR + lane] = sr;
+        __syncthreads();
+        float tot = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) tot += rsum[w * MR + (tid & (MR - 1))];
+        inv = 1.0f / sqrtf(tot / (float)K + p.norm_eps);
+    }
+
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u)
-        if (tid + u * NT < chunks) put(tid + u * NT, xv0[u]);
+        if (tid + u * NT < chunks) {
+            if constexpr (norm) {
+                const int q = chunk_q(tid + u * NT);
+                const float4* wk = reinterpret_cast<const float4*>(nws + (g0 + (q >> 2)) * 128 + (q & 3) * 32);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) xv0[u][t] = rms_apply8(xv0[u][t], wk[2 * t], wk[2 * t + 1], inv);
+            }
+            put(tid + u * NT, xv0[u]);
+        }
     for (int i0 = tid + NT * kStageUnroll; i0 < chunks; i0 += NT * kStageUnroll) {  // further rounds
         u32x4 xv[kStageUnroll][4];
 #pragma unroll
@@ -489,7 +549,14 @@ MbKernel mb_pick_nw(int nw) {
 }
 
 template <int EPI, typename OutT>
-MbKernel mb_kernel_for(int mr, int nw) {
+MbKernel mb_kernel_for(int mr, int nw, bool norm = false) {
+    if constexpr ((EPI == MB_PLAIN || EPI == MB_SWIGLU) && std::is_same<OutT, f16>::value) {
+        if (norm) {  // the planner keeps the norm to M = 4 / 8 at 4 or 8 waves
+            if (mr == 4) return nw >= 8 ? gemv_mb_int4_kernel<4, EPI, f16, 8, true> : gemv_mb_int4_kernel<4, EPI, f16, 4, true>;
+            return nw >= 8 ? gemv_mb_int4_kernel<8, EPI, f16, 8, true> : gemv_mb_int4_kernel<8, EPI, f16, 4, true>;
+        }
+    }
+    if (norm) return nullptr;
     if (mr <= 4) return mb_pick_nw<4, EPI, OutT>(nw);
     if (mr <= 8 || EPI == MB_ARGMAX) return mb_pick_nw<8, EPI, OutT>(nw);  // the LM head: M <= 8
     if constexpr (EPI != MB_ARGMAX) return mb_pick_nw<16, EPI, OutT>(nw);
@@ -569,6 +636,11 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     const int E = EPI == MB_SWIGLU ? 2 : 1;
     const int ng = p.K / 128;
     const int cus = num_cus();
+    // RMSNorm in the staging: only where a thread's staged chunks are all of
+    // one row (M a power of two, the row stride) and every row is whole in
+    // the block (one k-slice, checked below)
+    const bool norm = p.norm_w != nullptr;
+    if (norm && (EPI == MB_ARGMAX || (M != 4 && M != 8))) return false;
     int64_t tiles_total = 0;
     for (int i = 0; i < p.ndesc; ++i) tiles_total += (p.d[i].N + 15) / 16;
     const int mr = M <= 4 ? 4 : M <= 8 ? 8 : 16;
@@ -604,9 +676,11 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     int nw = ov.nw > 0 ? ov.nw : (EPI != MB_ARGMAX && slice > nw_at) ? 8 : 4;
     nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
     int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
+    // LDS of the norm: its weights and the waves' row sums
+    const size_t norm_lds = norm ? (size_t)p.K * 4 + 16 * 16 * 4 : 0;
     // never plan more blocks per CU than their X slices leave resident
     if (ov.bpc <= 0) {
-        const int fit = (int)(kMaxLds / (slice + 4096));
+        const int fit = (int)(kMaxLds / (slice + 4096 + norm_lds));
         if (fit < bpc) bpc = fit < 1 ? 1 : fit;
     }
     const int64_t target = (int64_t)cus * bpc;
@@ -687,7 +761,7 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
             }
             for (int kwc = 1; kwc <= kw_cap; kwc *= 2) {
                 if (tmin < nw / kwc) continue;  // a run of waves without a tile
-                const size_t l = (size_t)gps * xg + (size_t)tmax * 16 * M * E * 4 * kwc + 2 * nw * 4 + 16;
+                const size_t l = (size_t)gps * xg + (size_t)tmax * 16 * M * E * 4 * kwc + 2 * nw * 4 + 16 + norm_lds;
                 if (l * c > kMaxLds) continue;
                 const int64_t cc = cost(used * ks, tmax, kwc);
                 if (cc < best) {
@@ -702,8 +776,13 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     }
     int lkw = 0;
     while ((1 << lkw) < kw) ++lkw;
-    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16;
+    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16 + norm_lds;
     if (lds > kMaxLds) return false;
+    // the norm's single staging round: chunks and weights per thread within
+    // the kernel's unrolls (8 / 4 chunks at 4 / 8 waves, 1536 float4 of
+    // weights per block)
+    if (norm && (ks != 1 || nw > 8 || (int64_t)ng * 4 * M > (nw == 4 ? 8 : 4) * 64 * nw || p.K > 6144))
+        return false;
     if (ks > 1 && ranges > cnt_cap) return false;
     for (int i = 0; ks > 1 && i < p.ndesc; ++i)  // 32-bit buffer offsets into the partials
         if ((int64_t)ks * (E * M * p.d[i].N + 64) * 4 >= (1LL << 31)) return false;
@@ -715,7 +794,8 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     pl.nranges = (int)ranges;
     pl.kw = kw;
     pl.lds = lds;
-    pl.k = mb_kernel_for<EPI, OutT>(mr, nw);
+    pl.k = mb_kernel_for<EPI, OutT>(mr, nw, norm);
+    if (!pl.k) return false;
     int blocks = 0, rbeg = 0;
     int64_t wsoff = 0;
     for (int i = 0; i < p.ndesc; ++i) {
@@ -790,9 +870,11 @@ int launch_mb(const MbParams& p0, const MbPlan& pl, hipStream_t st) {
 // Entry points used by the GEMV front end (gemv_int4.hip).  Return 1 when the
 // shape is not handled here (the caller then runs the VALU GEMV).
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
-              int64_t M, int64_t K, bool residual, int* rc) {
+              int64_t M, int64_t K, bool residual, int* rc, const float* norm_w, float eps) {
     MbParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     p.M = (int32_t)M;
     p.K = (int32_t)K;
     p.ndesc = nd;
@@ -813,9 +895,11 @@ int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void
 
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
               const uint8_t* Wu, const void* Su, int64_t M, int64_t N, int64_t K,
-              int* rc) {
+              int* rc, const float* norm_w, float eps) {
     MbParams p = {};
     p.X = reinterpret_cast<const f16*>(X);
+    p.norm_w = norm_w;
+    p.norm_eps = eps;
     p.M = (int32_t)M;
     p.K = (int32_t)K;
     p.ndesc = 1;

@@ -899,6 +899,8 @@ int pairm_bpc(int64_t M, int64_t K, int64_t rows, bool swiglu) {
 }
 }  // namespace
 
+bool pairm_takes(int64_t M, int64_t K, int64_t rows, bool swiglu) { return pairm_bpc(M, K, rows, swiglu) > 0; }
+
 // M = 2..4 on the row-pair pattern (dot2 per row); returns 1 when the
 // shape is left to the other kernels.
 int pairm_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32, int64_t M,
