@@ -101,7 +101,7 @@ def _oracle_step(L, x_bits, M):
     return r, logits
 
 
-@pytest.mark.parametrize("M", [1, 4])
+@pytest.mark.parametrize("M", [1, 4, 8])
 def test_decode_step_graph_replays_match_eager(M):
     import torch
     from xinfer_amd import ops
