@@ -426,7 +426,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         rigs = [Rig(torch, dev, N, K, 0.02, seed=i) for i, N in enumerate(Ns)]
         copies = min(r.copies for r in rigs)
         nw = torch.linspace(0.5, 1.5, K, dtype=torch.float32, device=dev)
-        for M in (1, 4, 8):
+        for M in (1, 2, 4, 8):
             X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
             Xn = torch.empty_like(X)
             ws = torch.empty(max(1, M * K * 2), dtype=torch.uint8, device=dev)
@@ -447,7 +447,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         del rigs
         N, K = 17408, 5120                     # gate/up SwiGLU with the input norm
         rig = Rig(torch, dev, 2 * N, K, 0.02)
-        for M in (4, 8):
+        for M in (2, 4, 8):
             X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
             Xn = torch.empty_like(X)
             ws = torch.empty(M * K * 2, dtype=torch.uint8, device=dev)

@@ -963,14 +963,22 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
     }
     if (nd == 0) return XINFER_OK;
     if (int rc = check_norm_ws(norm_w, M, K, ws, ws_bytes)) return rc;
+    int64_t rows = 0;
+    for (int i = 0; i < nd; ++i) rows += live[i].N;
     // M = 4 / 8 on the small-batch kernel: the norm in its X staging (no
     // standalone norm launch) when it takes the shape whole
     if (norm_w && (M == 4 || M == 8) && M <= mb_max_m()) {
-        int64_t rows = 0;
-        for (int i = 0; i < nd; ++i) rows += live[i].N;
         int mrc = XINFER_OK;
         if (!pairm_takes(M, K, rows, false) && !mb_linear(st, live, nd, X0, false, M, K, false, &mrc, norm_w, eps))
             return mrc;
+    }
+    // M = 2 on the GEMV (X staged in LDS): the norm in its X staging
+    if (norm_w && M == 2 && xhip_host::gemv_stages_x(2, K) && !pairm_takes(2, K, rows, false)) {
+        p.X = reinterpret_cast<const f16*>(X0);
+        p.norm_w = norm_w;
+        p.norm_eps = eps;
+        p.ndesc = nd;
+        return gemv_f16<EPI_PLAIN, f16>(st, p, M);
     }
     const void* X = X0;
     bool norm_in_kernel = false;
@@ -1020,10 +1028,11 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
         int mrc = XINFER_OK;  // the norm in the small-batch kernel's X staging
         if (!mb_swiglu(st, Y, X0, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc, norm_w, eps)) return mrc;
     }
+    const bool gemv_norm2 = norm_w && M == 2 && gemv_stages_x(2, K) && !pairm_takes(2, K, 2 * N, true);
     const void* X = X0;
-    bool norm_in_kernel = false;
-    if ((rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel))) return rc;
-    if (M >= 2 && M <= mb_max_m()) {
+    bool norm_in_kernel = gemv_norm2;  // M = 2: the GEMV's X staging applies the norm
+    if (!gemv_norm2 && (rc = norm_input(st, X0, norm_w, eps, M, K, ws, ws_bytes, &X, &norm_in_kernel))) return rc;
+    if (M >= 2 && M <= mb_max_m() && !gemv_norm2) {
         int mrc = XINFER_OK;
         if (!pairm_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc)) return mrc;
         if (!mb_swiglu(st, Y, X, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc))
