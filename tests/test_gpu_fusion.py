@@ -112,7 +112,28 @@ def test_rmsnorm_fused_qkv_descs(M):
     assert np.array_equal(_bits(dX), x)          # the input itself is not normalised in place
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (3, 640, 17408),
+@pytest.mark.parametrize("M", [2, 3, 4])
+def test_rmsnorm_fused_short_rows(M):
+    """4096 output rows over three descriptors: the norm in the GEMV's staging
+    at M = 2, in the dot2 kernel's at M = 3, the norm kernel first at M = 4."""
+    import torch
+    ops = _ops()
+    K, Ns = 5120, (2048, 1024, 1024)
+    print("case", M, flush=True)
+    x, w = _xin(300 + M, M, K, 2.0), _norm_w(301, K, 0.5, 1.5)
+    descs, refs, outs = [], [], []
+    for p, N in enumerate(Ns):
+        W, S = synth.packed_weights(310 + p, N, K), synth.scales(310 + p, N, K)
+        refs.append(_ref_linear_after_norm(x, w, W, S, M, N, K))
+        Y = _empty((M, N), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(W), f16_dev(S), None, N))
+    ops.rmsnorm_linear_int4_fused(f16_dev(x), to_dev(w), 1e-6, descs, 3, M, K)
+    for Y, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Y), ref))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 17408, 5120), (2, 17408, 5120), (3, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (3, 640, 17408),
                                    (1, 640, 17408), (2, 640, 17408), (2, 4096, 5120), (1, 2048, 4096), (1, 4096, 6144),
                                    (8, 17408, 5120), (4, 2048, 6144), (8, 640, 4096),
                                    (8, 1024, 6144)])

@@ -341,13 +341,16 @@ int pair_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const vo
                 int64_t K, bool residual, const float* norm_w, float eps, int* rc);
 int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
                 const void* Su, int64_t N, int64_t K, const float* norm_w, float eps, int* rc);
+// norm_w: RMSNorm of X in the kernel's staging (fp16 outputs, M = 2, 3;
+// otherwise the shape is declined)
 int pairm_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32, int64_t M,
-                 int64_t K, bool residual, int* rc);
+                 int64_t K, bool residual, int* rc, const float* norm_w = nullptr, float eps = 0.0f);
 // whether pairm_linear / pairm_swiglu take M rows of K (before the even-N
 // check; rows = output rows over all descriptors, 2 N for the SwiGLU)
 bool pairm_takes(int64_t M, int64_t K, int64_t rows, bool swiglu);
 int pairm_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg, const uint8_t* Wu,
-                 const void* Su, int64_t M, int64_t N, int64_t K, int* rc);
+                 const void* Su, int64_t M, int64_t N, int64_t K, int* rc, const float* norm_w = nullptr,
+                 float eps = 0.0f);
 // XINFER_PAIR_SWIGLU=0 keeps the M = 1 gate/up SwiGLU on the GEMV (tuning)
 inline bool swiglu_pair_on() {
     static const bool on = [] {

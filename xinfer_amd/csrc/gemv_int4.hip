@@ -965,8 +965,13 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
     if (int rc = check_norm_ws(norm_w, M, K, ws, ws_bytes)) return rc;
     int64_t rows = 0;
     for (int i = 0; i < nd; ++i) rows += live[i].N;
-    // M = 4 / 8 on the small-batch kernel: the norm in its X staging (no
-    // standalone norm launch) when it takes the shape whole
+    // M = 2 / 3 on the dot2 kernel, M = 4 / 8 on the small-batch kernel:
+    // the norm in their X staging (no standalone norm launch) when they
+    // take the shape whole
+    if (norm_w && (M == 2 || M == 3) && M <= mb_max_m() && pairm_takes(M, K, rows, false)) {
+        int mrc = XINFER_OK;
+        if (!pairm_linear(st, live, nd, X0, false, M, K, false, &mrc, norm_w, eps)) return mrc;
+    }
     if (norm_w && (M == 4 || M == 8) && M <= mb_max_m()) {
         int mrc = XINFER_OK;
         if (!pairm_takes(M, K, rows, false) && !mb_linear(st, live, nd, X0, false, M, K, false, &mrc, norm_w, eps))
@@ -1024,6 +1029,10 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
         return XINFER_ERR_MISALIGNED;
     hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     if ((rc = check_norm_ws(norm_w, M, K, ws, ws_bytes))) return rc;
+    if (norm_w && (M == 2 || M == 3) && M <= mb_max_m() && pairm_takes(M, K, 2 * N, true)) {
+        int mrc = XINFER_OK;  // the norm in the dot2 kernel's X staging
+        if (!pairm_swiglu(st, Y, X0, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc, norm_w, eps)) return mrc;
+    }
     if (norm_w && (M == 4 || M == 8) && M <= mb_max_m() && !pairm_takes(M, K, 2 * N, true)) {
         int mrc = XINFER_OK;  // the norm in the small-batch kernel's X staging
         if (!mb_swiglu(st, Y, X0, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc, norm_w, eps)) return mrc;

@@ -162,8 +162,9 @@ def rmsnorm_linear_int4_fused(X: torch.Tensor, norm_weight: torch.Tensor, eps: f
                               descs: Sequence[FusedProjectionDesc], num_descs: int, M: int, K: int,
                               group_size: int = 128, workspace: Optional[torch.Tensor] = None,
                               stream=None) -> None:
-    """rmsnorm(X) then linear_int4_fused (one launch at M = 1; at M >= 2 the
-    normalised rows go through `workspace`, allocated here when not given)."""
+    """rmsnorm(X) then linear_int4_fused (one launch where the kernel taking
+    the shape applies the norm while it stages X; otherwise the normalised
+    rows go through `workspace`, allocated here when not given at M >= 2)."""
     L = load_library()
     ws, nws = _norm_workspace(X, M, K, workspace)
     arr = (FusedDesc * max(1, num_descs))()
