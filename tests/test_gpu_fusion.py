@@ -88,7 +88,7 @@ def _ref_linear_after_norm(x, w, W, S, M, N, K, bias=None):
     return oracle.linear_int4(xn, W, S, M, N, K, bias=bias, nthreads=cpu_threads())
 
 
-@pytest.mark.parametrize("M", [1, 2, 4, 8])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 6, 8])
 def test_rmsnorm_fused_qkv_descs(M):
     """Qwen3.5-27B full-attention shape (q 12288, k 1024, v 1024 at K 5120)
     with the input norm fused into the projection launch."""
