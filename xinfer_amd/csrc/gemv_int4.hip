@@ -893,12 +893,13 @@ int linear_f16_impl(void* stream, void* Y, bool y_f32, const void* X, const uint
 }
 
 // RMSNorm before a projection.  M = 1 (X staged whole by the GEMV): inside
-// the projection kernel, from the staged registers.  Otherwise the
-// standalone rmsnorm kernel writes the normalised rows to the caller's
-// workspace (M * K fp16), which the projection then reads: measured faster
-// at M >= 2 than a prologue inside the small-batch kernel (every block would
-// repeat the row reduction and the norm-weight reads before its first MFMA).
-// Returns the X the projection reads and whether the kernel applies the norm.
+// the projection kernel, from the staged registers; the fused entry points
+// below also route M = 2 / 3 (dot2 kernel, GEMV) and M = 4 / 8 (small-batch
+// kernel, one k-slice) to kernel variants that apply it while staging X.
+// Otherwise the standalone rmsnorm kernel writes the normalised rows to the
+// caller's workspace (M * K fp16), which the projection then reads.
+// norm_input returns the X the projection reads and whether the kernel
+// applies the norm (the M = 1 case).
 bool norm_in_projection(int64_t M, int64_t K) { return M == 1 && xhip_host::gemv_stages_x(1, K); }
 
 // The caller's workspace for the normalised rows, checked wherever the
