@@ -52,7 +52,8 @@ def _check_f32(y, ref):
 @pytest.mark.parametrize("M,N,K", [(2, 33, 128), (8, 17, 256), (3, 1000, 1536), (8, 4096, 5120),
                                    (6, 2000, 9984), (4, 5120, 17408), (7, 4100, 8192),
                                    (3, 5120, 6144), (4, 5120, 6144), (2, 2048, 4096), (4, 6144, 5120),
-                                   (3, 48, 4096), (4, 2048, 5120), (4, 4096, 4096)])
+                                   (3, 48, 4096), (4, 2048, 5120), (4, 4096, 4096), (2, 12288, 5120),
+                                   (2, 17410, 6144)])
 def test_small_batch_shapes(M, N, K):
     import torch
     ops = _ops()
