@@ -426,7 +426,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         rigs = [Rig(torch, dev, N, K, 0.02, seed=i) for i, N in enumerate(Ns)]
         copies = min(r.copies for r in rigs)
         nw = torch.linspace(0.5, 1.5, K, dtype=torch.float32, device=dev)
-        for M in (1, 2, 4, 8):
+        for M in (1, 2, 3, 4, 6, 8):
             X = torch.from_numpy(synth.activations(0, M, K)).view(torch.float16).to(dev)
             Xn = torch.empty_like(X)
             ws = torch.empty(max(1, M * K * 2), dtype=torch.uint8, device=dev)

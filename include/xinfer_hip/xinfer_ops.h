@@ -245,7 +245,7 @@ size_t xinfer_rmsnorm_projection_workspace_bytes(int64_t M, int64_t K);
  * the input-norm + QKV / linear-attention in_proj pair of forward.cpp:112-125
  * and :237-247.  The projections see exactly the fp16 normalised X that
  * xinfer_rmsnorm_f16 would write (up to the order of the sum of squares).
- * Any M: at M = 1 (and at M = 2 / 3 on the dot2 kernel or the GEMV, M = 4 / 8
+ * Any M: at M = 1 (and at M = 2 / 3 on the dot2 kernel or the GEMV, M = 3 / 4 / 8
  * with K <= 6144 on the small-batch kernel) the norm runs inside the
  * projection kernel; otherwise the normalised rows
  * go to `workspace`.  The workspace is checked at every M >= 2 (16-byte

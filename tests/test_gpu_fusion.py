@@ -136,7 +136,7 @@ def test_rmsnorm_fused_short_rows(M):
 @pytest.mark.parametrize("M,N,K", [(1, 17408, 5120), (2, 17408, 5120), (3, 17408, 5120), (4, 17408, 5120), (8, 1000, 1024), (3, 640, 17408),
                                    (1, 640, 17408), (2, 640, 17408), (2, 4096, 5120), (1, 2048, 4096), (1, 4096, 6144),
                                    (8, 17408, 5120), (4, 2048, 6144), (8, 640, 4096),
-                                   (8, 1024, 6144)])
+                                   (8, 1024, 6144), (5, 2048, 5120), (7, 4096, 4096), (3, 1024, 5120)])
 def test_rmsnorm_fused_swiglu(M, N, K):
     import torch
     from scipy.special import expit

@@ -834,8 +834,8 @@ int gemv_f16(hipStream_t st, const GemvParams& base, int64_t M) {
 // the MFMA small-batch kernel for 2 <= M <= 8 (gemv_mb_int4.hip; each returns
 // 1 when the shape is left to the VALU GEMV here).
 namespace xhip_host {
-// norm_w: RMSNorm of X inside the kernel (M = 4 or 8 with every row whole
-// in one block; otherwise the shape is declined)
+// norm_w: RMSNorm of X inside the kernel (M = 3, 4, 8 with every row whole in
+// one block; otherwise the shape is declined)
 int mb_linear(hipStream_t st, const xinfer_fused_desc* descs, int nd, const void* X, bool y_f32,
               int64_t M, int64_t K, bool residual, int* rc, const float* norm_w = nullptr, float eps = 0.0f);
 int mb_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const void* Sg,
@@ -966,14 +966,14 @@ int fused_f16_impl(void* stream, const void* X0, const xinfer_fused_desc* descs,
     if (int rc = check_norm_ws(norm_w, M, K, ws, ws_bytes)) return rc;
     int64_t rows = 0;
     for (int i = 0; i < nd; ++i) rows += live[i].N;
-    // M = 2 / 3 on the dot2 kernel, M = 4 / 8 on the small-batch kernel:
+    // M = 2 / 3 on the dot2 kernel, M = 3 / 4 / 8 on the small-batch kernel:
     // the norm in their X staging (no standalone norm launch) when they
     // take the shape whole
     if (norm_w && (M == 2 || M == 3) && M <= mb_max_m() && pairm_takes(M, K, rows, false)) {
         int mrc = XINFER_OK;
         if (!pairm_linear(st, live, nd, X0, false, M, K, false, &mrc, norm_w, eps)) return mrc;
     }
-    if (norm_w && (M == 4 || M == 8) && M <= mb_max_m()) {
+    if (norm_w && M >= 3 && M <= 8 && M <= mb_max_m()) {
         int mrc = XINFER_OK;
         if (!pairm_takes(M, K, rows, false) && !mb_linear(st, live, nd, X0, false, M, K, false, &mrc, norm_w, eps))
             return mrc;
@@ -1034,7 +1034,7 @@ int swiglu_f16_impl(void* stream, void* Y, const void* X0, const uint8_t* W_gate
         int mrc = XINFER_OK;  // the norm in the dot2 kernel's X staging
         if (!pairm_swiglu(st, Y, X0, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc, norm_w, eps)) return mrc;
     }
-    if (norm_w && (M == 4 || M == 8) && M <= mb_max_m() && !pairm_takes(M, K, 2 * N, true)) {
+    if (norm_w && M >= 3 && M <= 8 && M <= mb_max_m() && !pairm_takes(M, K, 2 * N, true)) {
         int mrc = XINFER_OK;  // the norm in the small-batch kernel's X staging
         if (!mb_swiglu(st, Y, X0, W_gate, scales_gate, W_up, scales_up, M, N, K, &mrc, norm_w, eps)) return mrc;
     }

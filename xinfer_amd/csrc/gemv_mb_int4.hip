@@ -114,7 +114,7 @@ __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
     return r;
 }
 
-template <int MR, int EPI, typename OutT, int NW, bool NORM = false>
+template <int MR, int EPI, typename OutT, int NW, int NORM = 0>
 __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p) {
     constexpr int E = (EPI == MB_SWIGLU) ? 2 : 1;  // sums per output (weight tiles per item)
     constexpr int NT = 64 * NW;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
         if (tid + u * NT < chunks) get(tid + u * NT, xv0[u]);
     // RMSNorm weights: requested with X, stored to LDS once they land (the
     // host keeps K <= 6144: K / 4 <= kNormPT * NT)
-    constexpr bool norm = NORM;  // p.norm_w set
+    constexpr bool norm = NORM != 0;  // p.norm_w set; NORM = 1: M == MR, 2: M < MR
     constexpr int kNormPT = 1536 / NT;
     float4 nwv[kNormPT];
 #pragma unroll
@@ -278,13 +278,16 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
 
     // RMSNorm prologue (fused norm + projection entry points; the host
-    // plans one k-slice, M == MR and one staging round, so a thread's
-    // chunks are all of row tid % MR and the block holds every row whole):
-    // the row's sum of squares in a fixed order (a thread's chunks, the
-    // lanes of the row in xor order, the waves in order), then x * inv * w
+    // plans one k-slice and one staging round, so the block holds every row
+    // whole): the rows' sums of squares in a fixed order, then x * inv * w
     // rounded to fp16 per element as the standalone norm does
-    // (src/ops/rmsnorm.cpp:45-78).
+    // (src/ops/rmsnorm.cpp:45-78).  M == MR: a thread's chunks are all of
+    // row tid % MR (its chunks, the row's lanes in xor order, the waves in
+    // order).  Otherwise each chunk's sum goes to LDS and one wave per row
+    // adds the row's chunks (lanes over the chunks in order, then the
+    // 64-lane reduction), leaving 1/rms per row in LDS.
     float inv = 0.0f;
+    float* css = rsum + 256;  // M != MR: per-chunk sums of squares
     if constexpr (norm) {
 #pragma unroll
         for (int u = 0; u < kNormPT; ++u)
@@ -293,23 +296,42 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 #pragma unroll
         for (int u = 0; u < kStageUnroll; ++u)
             if (tid + u * NT < chunks) {
+                float c0 = 0.0f, c1 = 0.0f;
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
-                    s0 = dot2(as_h2(xv0[u][t].x), as_h2(xv0[u][t].x), s0);
-                    s1 = dot2(as_h2(xv0[u][t].y), as_h2(xv0[u][t].y), s1);
-                    s0 = dot2(as_h2(xv0[u][t].z), as_h2(xv0[u][t].z), s0);
-                    s1 = dot2(as_h2(xv0[u][t].w), as_h2(xv0[u][t].w), s1);
+                    c0 = dot2(as_h2(xv0[u][t].x), as_h2(xv0[u][t].x), c0);
+                    c1 = dot2(as_h2(xv0[u][t].y), as_h2(xv0[u][t].y), c1);
+                    c0 = dot2(as_h2(xv0[u][t].z), as_h2(xv0[u][t].z), c0);
+                    c1 = dot2(as_h2(xv0[u][t].w), as_h2(xv0[u][t].w), c1);
+                }
+                if constexpr (NORM == 1) {
+                    s0 += c0;
+                    s1 += c1;
+                } else {
+                    css[tid + u * NT] = c0 + c1;
                 }
             }
-        float sr = s0 + s1;
+        if constexpr (NORM == 1) {
+            float sr = s0 + s1;
 #pragma unroll
-        for (int off = MR; off < 64; off <<= 1) sr += __shfl_xor(sr, off);
-        if (lane < MR) rsum[wave * MR + lane] = sr;
-        __syncthreads();
-        float tot = 0.0f;
+            for (int off = MR; off < 64; off <<= 1) sr += __shfl_xor(sr, off);
+            if (lane < MR) rsum[wave * MR + lane] = sr;
+            __syncthreads();
+            float tot = 0.0f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) tot += rsum[w * MR + (tid & (MR - 1))];
-        inv = 1.0f / sqrtf(tot / (float)K + p.norm_eps);
+            for (int w = 0; w < NW; ++w) tot += rsum[w * MR + (tid & (MR - 1))];
+            inv = 1.0f / sqrtf(tot / (float)K + p.norm_eps);
+        } else {
+            __syncthreads();
+            const int nq = chunks / M;  // chunks per row
+            for (int m = wave; m < M; m += NW) {
+                float sv[1] = {0.0f};
+                for (int q = lane; q < nq; q += 64) sv[0] += css[q * M + m];
+                const float t = wave_sum_multi<1>(sv, lane);
+                if (lane == 0) rsum[m] = 1.0f / sqrtf(t / (float)K + p.norm_eps);
+            }
+            __syncthreads();
+        }
     }
 
 #pragma unroll
@@ -317,9 +339,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
         if (tid + u * NT < chunks) {
             if constexpr (norm) {
                 const int q = chunk_q(tid + u * NT);
+                float iv = inv;
+                if constexpr (NORM == 2) iv = rsum[chunk_m(tid + u * NT)];
                 const float4* wk = reinterpret_cast<const float4*>(nws + (g0 + (q >> 2)) * 128 + (q & 3) * 32);
 #pragma unroll
-                for (int t = 0; t < 4; ++t) xv0[u][t] = rms_apply8(xv0[u][t], wk[2 * t], wk[2 * t + 1], inv);
+                for (int t = 0; t < 4; ++t) xv0[u][t] = rms_apply8(xv0[u][t], wk[2 * t], wk[2 * t + 1], iv);
             }
             put(tid + u * NT, xv0[u]);
         }
@@ -549,12 +573,14 @@ MbKernel mb_pick_nw(int nw) {
 }
 
 template <int EPI, typename OutT>
-MbKernel mb_kernel_for(int mr, int nw, bool norm = false) {
+MbKernel mb_kernel_for(int mr, int nw, int norm = 0) {
     if constexpr ((EPI == MB_PLAIN || EPI == MB_SWIGLU) && std::is_same<OutT, f16>::value) {
-        if (norm) {  // the planner keeps the norm to M = 4 / 8 at 4 or 8 waves
-            if (mr == 4) return nw >= 8 ? gemv_mb_int4_kernel<4, EPI, f16, 8, true> : gemv_mb_int4_kernel<4, EPI, f16, 4, true>;
-            return nw >= 8 ? gemv_mb_int4_kernel<8, EPI, f16, 8, true> : gemv_mb_int4_kernel<8, EPI, f16, 4, true>;
+        if (norm == 1) {  // M == MR (4 or 8) at 4 or 8 waves
+            if (mr == 4) return nw >= 8 ? gemv_mb_int4_kernel<4, EPI, f16, 8, 1> : gemv_mb_int4_kernel<4, EPI, f16, 4, 1>;
+            return nw >= 8 ? gemv_mb_int4_kernel<8, EPI, f16, 8, 1> : gemv_mb_int4_kernel<8, EPI, f16, 4, 1>;
         }
+        if (norm == 2 && mr == 4)  // M = 3
+            return nw >= 8 ? gemv_mb_int4_kernel<4, EPI, f16, 8, 2> : gemv_mb_int4_kernel<4, EPI, f16, 4, 2>;
     }
     if (norm) return nullptr;
     if (mr <= 4) return mb_pick_nw<4, EPI, OutT>(nw);
@@ -636,11 +662,13 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     const int E = EPI == MB_SWIGLU ? 2 : 1;
     const int ng = p.K / 128;
     const int cus = num_cus();
-    // RMSNorm in the staging: only where a thread's staged chunks are all of
-    // one row (M a power of two, the row stride) and every row is whole in
-    // the block (one k-slice, checked below)
+    // RMSNorm in the staging: every row whole in the block (one k-slice and
+    // one staging round, checked below)
     const bool norm = p.norm_w != nullptr;
-    if (norm && (EPI == MB_ARGMAX || (M != 4 && M != 8))) return false;
+    // (M = 4 / 8: a thread's chunks are all of one row; M = 3: per-chunk
+    // sums through LDS; at M = 5-7 that form measured no faster than the
+    // norm kernel first)
+    if (norm && (EPI == MB_ARGMAX || (M != 3 && M != 4 && M != 8))) return false;
     int64_t tiles_total = 0;
     for (int i = 0; i < p.ndesc; ++i) tiles_total += (p.d[i].N + 15) / 16;
     const int mr = M <= 4 ? 4 : M <= 8 ? 8 : 16;
@@ -677,7 +705,7 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
     int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
     // LDS of the norm: its weights and the waves' row sums
-    const size_t norm_lds = norm ? (size_t)p.K * 4 + 16 * 16 * 4 : 0;
+    const size_t norm_lds = norm ? (size_t)p.K * 4 + 256 * 4 + (size_t)ng * 4 * M * 4 : 0;
     // never plan more blocks per CU than their X slices leave resident
     if (ov.bpc <= 0) {
         const int fit = (int)(kMaxLds / (slice + 4096 + norm_lds));
@@ -794,7 +822,7 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     pl.nranges = (int)ranges;
     pl.kw = kw;
     pl.lds = lds;
-    pl.k = mb_kernel_for<EPI, OutT>(mr, nw, norm);
+    pl.k = mb_kernel_for<EPI, OutT>(mr, nw, !norm ? 0 : M == mr ? 1 : 2);
     if (!pl.k) return false;
     int blocks = 0, rbeg = 0;
     int64_t wsoff = 0;
