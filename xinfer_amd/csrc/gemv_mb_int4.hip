@@ -272,7 +272,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             nwv[u] = reinterpret_cast<const float4*>(p.norm_w)[min(tid + u * NT, (K >> 2) - 1)];
     }
 
-    constexpr int PF = XHIP_MB_PF;  // items in flight per wave
+    // items in flight per wave: a SwiGLU item carries both matrices' groups
+    // (twice the bytes), and one item less measured faster there (gate/up
+    // M = 4 / 8 28.9 / 31.4 -> 28.2 / 30.3 us) while the plain and argmax
+    // forms lost 1.5-4.6 % with it
+    constexpr int PF = EPI == MB_SWIGLU ? XHIP_MB_PF - 1 : XHIP_MB_PF;
     MbItem<E> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
