@@ -202,14 +202,31 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     set_tile(t0);
     int lt = t0, lg = 0, lrem = nreal;  // load cursor (wave-uniform): tile, item, items left
     auto load_next = [&](MbItem<E>& b) {
-#pragma unroll
-        for (int gi = 0; gi < kGP; ++gi) {
-            const int g = min(lg * kGP + gi, ngw - 1);
+        if constexpr (E == 2) {
+            // SwiGLU: a matrix's two groups (the two halves of each row's
+            // 128-byte line) back to back, then the other matrix's (gate/up
+            // M = 4 / 8 28.1 / 30.3 -> 26.75 / 29.2 us against alternating
+            // matrices); the plain form keeps each group's scale next to it
 #pragma unroll
             for (int e = 0; e < E; ++e) {
-                b.w[e * kGP + gi] =
-                    __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)vw, g * 64, XHIP_MB_AUX);
-                b.s[e * kGP + gi] = __builtin_amdgcn_raw_buffer_load_b16(e ? rs1 : rs0, (int)vs, g * 2, 0);
+#pragma unroll
+                for (int gi = 0; gi < kGP; ++gi) {
+                    const int g = min(lg * kGP + gi, ngw - 1);
+                    b.w[e * kGP + gi] =
+                        __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)vw, g * 64, XHIP_MB_AUX);
+                }
+#pragma unroll
+                for (int gi = 0; gi < kGP; ++gi) {
+                    const int g = min(lg * kGP + gi, ngw - 1);
+                    b.s[e * kGP + gi] = __builtin_amdgcn_raw_buffer_load_b16(e ? rs1 : rs0, (int)vs, g * 2, 0);
+                }
+            }
+        } else {
+#pragma unroll
+            for (int gi = 0; gi < kGP; ++gi) {
+                const int g = min(lg * kGP + gi, ngw - 1);
+                b.w[gi] = __builtin_amdgcn_raw_buffer_load_b128(rw0, (int)vw, g * 64, XHIP_MB_AUX);
+                b.s[gi] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vs, g * 2, 0);
             }
         }
         // past the last item the cursor stays: the extra loads repeat it
