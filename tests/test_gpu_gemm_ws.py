@@ -2,7 +2,10 @@
 the oracle at the BASELINE fp16 bound (max abs <= 1e-2, rel-L2 <= 1e-3).
 The default routing sends only shapes that fill the CUs to it (config 4);
 a child process with XINFER_GEMM_WS=1 forces it for ragged shapes: M and N
-off the 128 x 272 block, a partial 17th tile, bias and the residual form."""
+off the 256 x 136 block (a partial last row block, N below one block and
+not a multiple of 8, partial last column blocks), bias, the residual form,
+and an output view 2 bytes past a 16-byte boundary (the per-element store
+path instead of 16-byte stores)."""
 import os
 import subprocess
 import sys
@@ -40,7 +43,7 @@ def f16(a):
 def bits(t):
     return t.cpu().view(torch.int16).numpy().view(np.uint16)
 shapes = [(17, 272, 1024), (128, 544, 1024), (130, 300, 2048), (200, 560, 1024), (257, 1000, 3072),
-          (64, 17, 1024), (512, 4352, 2048)]
+          (64, 17, 1024), (512, 4352, 2048), (300, 408, 1024), (512, 136, 5120)]
 for (M, N, K) in shapes:
     print("case", M, N, K, flush=True)
     W, S, Xb = synth.packed_weights(M + N, N, K), synth.scales(M + N, N, K), synth.activations(M, M, K)
@@ -61,6 +64,12 @@ for (M, N, K) in shapes:
     ops.linear_int4(Yp, dX, dW, dS, None, M, N, K)
     want = (Yp.float() + f16(R0).float()).half()
     assert torch.equal(R, want), (M, N, K)
+    # an output view 2 bytes past a 16-byte boundary
+    Yb = torch.full((M * N + 8,), float("nan"), dtype=torch.float16, device=dev)
+    Yo = Yb[1:1 + M * N].view(M, N)
+    ops.linear_int4(Yo, dX, dW, dS, torch.from_numpy(bias).to(dev), M, N, K)
+    assert torch.equal(Yo, Y), (M, N, K, "offset view")
+    assert torch.isnan(Yb[0]) and torch.isnan(Yb[1 + M * N:]).all(), (M, N, K, "outside the view")
     print("ok", M, N, K, err, rl2, flush=True)
 print("ws child ok")
 """
