@@ -29,6 +29,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -566,10 +567,29 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
         fn = lambda i: ops.linear_int4(Y, X, rig.W[i], rig.S[i], None, M, N, K)  # noqa: E731
         w, e = time_launches(torch, fn, max(32, steps // 4), 8, rig.copies, graph=graph)
         fl = 2 * M * N * K
-        record("cfg4_prefill_m512_n17408_k5120",
+        exact_route = os.environ.get("XINFER_GEMM_EXACT") == "1"
+        record("cfg4_prefill_exact_dequant_m512_n17408_k5120" if exact_route else "cfg4_prefill_m512_n17408_k5120",
                {"M": M, "N": N, "K": K, "us": round(e * 1e6, 2), "TFLOPs": round(fl / e / 1e12, 1),
                 "frac_fp16_mfma": round(fl / e / 1e12 / FP16_PEAK_TFLOPS, 4),
-                "kernel": "xhip::gemm_ws_int4_kernel (256x136 blocks, producer/consumer waves)"})
+                "kernel": ("xhip::gemm_int4_mfma_kernel<EXACT> (exact q, FP32 group scale; 128-row blocks)"
+                           if exact_route else
+                           "xhip::gemm_ws_int4_kernel (256x136 blocks; 4 MFMA waves copying their own X "
+                           "rows, 4 weight-decode waves; B = fp16(q*s))")})
+        if not exact_route:
+            # the same projection with the reference's dequantisation (exact
+            # integer q, FP32 group scale) on the other GEMM kernel, in a
+            # child process (the route is chosen from the environment once)
+            env = dict(os.environ, XINFER_GEMM_WS="0", XINFER_GEMM_EXACT="1")
+            r = subprocess.run([sys.executable, os.path.abspath(__file__), "--only", "cfg4", "--no-cpu",
+                                "--steps", str(args.steps), "--warmup", str(args.warmup)]
+                               + (["--eager"] if args.eager else []),
+                               capture_output=True, text=True, env=env, timeout=300)
+            try:
+                sub = json.loads(r.stdout.strip().splitlines()[-1])["suite"]
+                for k, v in sub.items():
+                    record(k, v)
+            except Exception as ex:  # noqa: BLE001 (reported, not fatal to the headline)
+                log(f"  exact-dequant child failed: {ex}: {r.stderr[-500:]}")
     return out
 
 

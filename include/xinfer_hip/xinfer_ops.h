@@ -26,16 +26,21 @@
  * No projection entry point allocates device memory or synchronises: the
  * first call of any shape can be captured into a hipGraph.  The small-batch
  * kernel's cross-block split-K partials live in a static device array that
- * the code object loader places with the library's kernels (32 slots per
- * device, one owned by each stream that calls; with more streams than slots
- * a call plans without the cross-block split).  Calls on different streams
- * may therefore overlap.  A graph holds the slot of the stream it was
- * captured on: replays of graphs captured on one stream must not overlap
- * each other or that stream's work.  The only allocating calls are
- * xinfer_argmax_f32 and xinfer_lm_head_argmax_int4 given scratch == NULL
- * (a library-owned buffer per device and stream, grown on demand, as the
- * reference's argmax falls back to its own allocation,
- * src/ops/sampling.cpp:28-31); pass scratch to keep them capturable.
+ * the code object loader places with the library's kernels: 32 slots of
+ * 4 MiB + 16 KiB (128.5 MiB) on every device the library runs on, one
+ * owned by each stream that calls until xinfer_stream_release gives it
+ * back; with every slot owned a call plans without the cross-block split
+ * (correct, slower).  Calls on different streams may therefore overlap.  A
+ * graph holds the slot of the stream it was captured on: replays of graphs
+ * captured on one stream must not overlap each other or that stream's work
+ * (a decode-step graph replayed in order on its own stream, as the
+ * reference's DecodeGraph does, src/targets/qwen3_8/decode_graph.cpp:9-12,
+ * never does).  The only allocating calls are xinfer_argmax_f32 and
+ * xinfer_lm_head_argmax_int4 given scratch == NULL (a library-owned buffer
+ * per device and stream, grown on demand -- growing waits for the stream and
+ * frees the old buffer -- as the reference's argmax falls back to its own
+ * allocation, src/ops/sampling.cpp:28-31); pass scratch to keep them
+ * capturable.
  * The RMSNorm + projection entry points take a caller-owned workspace for
  * the normalised rows (the reference's forward_layer writes them to an
  * arena buffer, src/targets/qwen3_8/forward.cpp:112-125).
@@ -60,6 +65,14 @@ extern "C" {
 /* Human-readable name of a status code (static string). */
 const char* xinfer_status_string(int status);
 
+/* No counterpart in the reference (its queues are created once per
+ * DeviceContext and never destroyed).  For long-running callers that create
+ * and destroy streams: waits for `stream`'s work, then gives back its
+ * split-K slot and frees its argmax scratch on the current device, so a
+ * later stream can take them.  Call it before hipStreamDestroy; without it a
+ * destroyed stream keeps its slot until the process ends. */
+int xinfer_stream_release(void* stream);
+
 /* Library version string, e.g. "xinfer_hip 0.1.0 gfx950". */
 const char* xinfer_version(void);
 
@@ -69,8 +82,11 @@ const char* xinfer_version(void);
  * M <= 16 runs the bandwidth-bound decode kernels (VALU GEMV at M = 1-2,
  * MFMA small-batch kernel at M = 2-16); larger M (chunked prefill) runs the
  * MFMA GEMM, as the reference routes both through this one call
- * (src/targets/qwen3_8/forward.cpp:284-287).  The fp32-output GEMM rounds
- * q*s to fp16 once per weight (the decode kernels scale in FP32).
+ * (src/targets/qwen3_8/forward.cpp:284-287).  Dequantisation: the decode
+ * kernels (M <= 16) and fp32 outputs at any M multiply the exact integer q
+ * by the FP32 group scale, as the reference does; the fp16-output prefill
+ * GEMM (M > 16) feeds the matrix cores B = fp16(q*s), rounded once per
+ * weight (relative error <= 2^-11, inside the fp16 output's rounding).
  * ------------------------------------------------------------------------- */
 
 /* Replaces `sycl::event linear_int4(sycl::queue&, sycl::half* Y,

@@ -14,6 +14,7 @@ and within the fp32-output bound of the oracle.  Forty streams exceed the
 library's 32 split-K slots per device: the extra streams plan without the
 cross-block split (another summation order, so other bits than the solo
 run), and every one of their results must match the oracle and each other."""
+import ctypes
 import os
 import subprocess
 import sys
@@ -111,7 +112,16 @@ def test_concurrent_streams_small_batch(nstreams):
             for (W, S, Xb) in (x[:3] for x in ins)]
     for i in range(nstreams):
         _check_f32(solo[i], refs[i])
-    streams = [torch.cuda.Stream() for _ in range(nstreams)]
+    # raw HIP streams (torch's pool hands out at most 32 distinct streams per
+    # priority, so 40 torch streams would repeat handles)
+    hip = ctypes.CDLL("libamdhip64.so")
+    handles = []
+    for _ in range(nstreams):
+        h = ctypes.c_void_p()
+        assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+        handles.append(h.value)
+    assert len(set(handles)) == nstreams
+    streams = handles
     outs = [[torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda") for _ in range(reps)]
             for _ in range(nstreams)]
     torch.cuda.synchronize()
@@ -130,3 +140,19 @@ def test_concurrent_streams_small_batch(nstreams):
     print("streams with the solo run's bits:", exact, "of", nstreams)
     if nstreams <= 2:  # both streams hold a split-K slot: the solo plan
         assert exact == nstreams
+    else:  # more streams than slots: some ran the plan without the cross-block split
+        assert exact < nstreams
+    # giving the slots back lets new streams take them: after the release a
+    # fresh stream runs the split-K plan again (the solo run's bits)
+    for h in handles:
+        ops.stream_release(h)
+        assert hip.hipStreamDestroy(ctypes.c_void_p(h)) == 0
+    h = ctypes.c_void_p()
+    assert hip.hipStreamCreate(ctypes.byref(h)) == 0
+    _, _, _, dW, dS, dX = ins[0]
+    Y = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
+    ops.linear_int4(Y, dX, dW, dS, None, M, N, K, stream=h.value)
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(Y).view(np.uint32), solo[0].view(np.uint32))
+    ops.stream_release(h.value)
+    assert hip.hipStreamDestroy(h) == 0

@@ -24,6 +24,7 @@ XINFER_ERR_CHECKSUM = -7
 EXPORTS = (
     "xinfer_status_string",
     "xinfer_version",
+    "xinfer_stream_release",
     "xinfer_linear_int4_f16",
     "xinfer_linear_int4_f16_f32out",
     "xinfer_linear_int4_f32",
@@ -130,6 +131,8 @@ def load_library(path: str = None):
     L.xinfer_status_string.argtypes = [ctypes.c_int]
     L.xinfer_version.restype = ctypes.c_char_p
     L.xinfer_version.argtypes = []
+    L.xinfer_stream_release.restype = ctypes.c_int
+    L.xinfer_stream_release.argtypes = [_p]
     lin = [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i32]
     for n in ("xinfer_linear_int4_f16", "xinfer_linear_int4_f16_f32out",
               "xinfer_linear_int4_f32", "xinfer_linear_int4_naive_f32"):

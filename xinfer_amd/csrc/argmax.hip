@@ -91,28 +91,42 @@ namespace xhip_host {
 
 // Library-owned scratch for callers that pass scratch == NULL: one buffer
 // per device and stream (so calls on different streams never share it),
-// grown on demand and never freed while the process runs (a smaller old
-// buffer is kept alive because work already queued may still use it).
-// Returns nullptr when the allocation fails or more than kStreams streams of
-// a device ask for one.
+// grown on demand.  Growing waits for the stream's queued work (which may
+// still read the old buffer) and frees the old buffer before allocating the
+// new one; xinfer_stream_release frees a stream's buffer.  Returns nullptr
+// when the allocation fails or more than kStreams streams of a device hold
+// one.
+namespace {
+constexpr int kScratchStreams = 16;
+struct ScratchEntry { hipStream_t st; void* buf; size_t cap; };
+std::mutex g_scratch_mu;
+ScratchEntry g_scratch[64][kScratchStreams];
+int g_nscratch[64] = {0};
+}  // namespace
+
 void* library_scratch(hipStream_t st, size_t bytes) {
-    constexpr int kStreams = 16;
-    struct Entry { hipStream_t st; void* buf; size_t cap; };
-    static std::mutex mu;
-    static Entry tab[64][kStreams];
-    static int n[64] = {0};
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
-    std::lock_guard<std::mutex> lock(mu);
-    Entry* e = nullptr;
-    for (int i = 0; i < n[dev]; ++i)
-        if (tab[dev][i].st == st) e = &tab[dev][i];
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ScratchEntry* e = nullptr;
+    for (int i = 0; i < g_nscratch[dev]; ++i)
+        if (g_scratch[dev][i].st == st && g_scratch[dev][i].buf) e = &g_scratch[dev][i];
     if (!e) {
-        if (n[dev] == kStreams) return nullptr;
-        e = &tab[dev][n[dev]++];
-        *e = Entry{st, nullptr, 0};
+        for (int i = 0; i < g_nscratch[dev] && !e; ++i)
+            if (!g_scratch[dev][i].buf) e = &g_scratch[dev][i];  // a released entry
+        if (!e) {
+            if (g_nscratch[dev] == kScratchStreams) return nullptr;
+            e = &g_scratch[dev][g_nscratch[dev]++];
+        }
+        *e = ScratchEntry{st, nullptr, 0};
     }
     if (e->cap < bytes) {
+        if (e->buf) {
+            if (hipStreamSynchronize(st) != hipSuccess) return nullptr;
+            (void)hipFree(e->buf);
+            e->buf = nullptr;
+            e->cap = 0;
+        }
         size_t want = bytes < (1u << 20) ? (1u << 20) : bytes * 2;
         void* p = nullptr;
         if (hipMalloc(&p, want) != hipSuccess) return nullptr;
@@ -122,9 +136,33 @@ void* library_scratch(hipStream_t st, size_t bytes) {
     return e->buf;
 }
 
+// Frees the library scratch of `st` on the current device (after its work).
+void library_scratch_release(hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    for (int i = 0; i < g_nscratch[dev]; ++i) {
+        ScratchEntry& e = g_scratch[dev][i];
+        if (e.st == st && e.buf) {
+            (void)hipFree(e.buf);
+            e = ScratchEntry{nullptr, nullptr, 0};
+        }
+    }
+}
+
+void splitk_release(hipStream_t st);  // scratch.hip
+
 }  // namespace xhip_host
 
 extern "C" {
+
+int xinfer_stream_release(void* stream) {
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    if (hipStreamSynchronize(st) != hipSuccess) return XINFER_ERR_HIP;
+    xhip_host::splitk_release(st);
+    xhip_host::library_scratch_release(st);
+    return XINFER_OK;
+}
 
 size_t xinfer_argmax_scratch_bytes(int64_t V, int64_t rows) {
     if (V <= 1 || rows <= 0) return 0;

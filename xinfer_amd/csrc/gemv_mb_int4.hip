@@ -480,19 +480,22 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
                     (int)(((uint32_t)slice * sst + ((uint32_t)x * M + m) * (uint32_t)N + n0 + rl) * 4u), 0,
                     kDeviceCoherent);
         }
-        // The partials are written and read only with device-coherent (sc1)
-        // accesses, the form of agent-scope atomic stores and loads, so they
-        // are consistent across the XCDs' L2s without a release write-back or
-        // an acquire invalidate of the L2.  Each wave waits for its stores to
-        // be acknowledged before the barrier, and the arrival is counted
-        // after the barrier; the last arriver's loads are issued after it has
-        // seen the count (control dependency through the flag).
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // Arrival protocol on the memory model: the block's partial stores
+        // happen before thread 0's arrival (workgroup barrier); the arrival
+        // is an agent-scope release fetch_add, and the last arriver (the one
+        // that counts ks - 1) issues an agent-scope acquire fence, so every
+        // arriver's partials happen before the last arriver's loads (for its
+        // other threads through the workgroup barrier after the fence).  The
+        // partials also move with device-coherent (sc1) accesses, so the
+        // release / acquire find no dirty or stale lines of theirs in the
+        // XCDs' L2s.
         __syncthreads();
         if (tid == 0) {
-            const uint32_t old = __hip_atomic_fetch_add(&p.cnt[grange], 1u, __ATOMIC_RELAXED,
+            const uint32_t old = __hip_atomic_fetch_add(&p.cnt[grange], 1u, __ATOMIC_RELEASE,
                                                         __HIP_MEMORY_SCOPE_AGENT);
-            flag[0] = (old == (uint32_t)(ks - 1)) ? 1 : 0;
+            const bool last = old == (uint32_t)(ks - 1);
+            if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            flag[0] = last ? 1 : 0;
         }
         __syncthreads();
         if (flag[0] == 0) return;  // another slice of this range finishes it

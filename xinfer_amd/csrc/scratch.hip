@@ -10,13 +10,14 @@
 // the first call of a shape can be captured into a hipGraph.
 //
 // The array holds kSplitSlots independent slots (partials + arrival
-// counters).  A slot belongs to one stream of a device for the life of the
-// process: calls on one stream run in order, so they never share a slot
-// concurrently, and calls on different streams use different slots.  Every
-// counter is zero at load time and is returned to zero by the block that
-// finishes its tile range, so a slot needs no clearing between calls.
-// When every slot of a device is taken (more streams than slots) the caller
-// plans without a cross-block split instead.
+// counters), 32 x (4 MiB + 16 KiB) = 128.5 MiB on every device the library
+// runs on.  A slot belongs to one stream of a device until
+// xinfer_stream_release gives it back: calls on one stream run in order, so
+// they never share a slot concurrently, and calls on different streams use
+// different slots.  Every counter is zero at load time and is returned to
+// zero by the block that finishes its tile range, so a slot needs no
+// clearing between calls.  When every slot of a device is taken (more live
+// streams than slots) the caller plans without a cross-block split instead.
 
 #include <mutex>
 
@@ -41,7 +42,10 @@ struct DevSlots {
     uint32_t* counters = nullptr; // device address of g_splitk_counters on this device
     int nused = 0;
     hipStream_t owner[xhip::kSplitSlots] = {};
+    bool released[xhip::kSplitSlots] = {};
 };
+std::mutex g_mu;
+DevSlots g_devs[kMaxDev];
 }  // namespace
 
 // The split-K slot of `st` on the current device: its partials (capacity in
@@ -49,12 +53,10 @@ struct DevSlots {
 // all owned by other streams or the symbol lookup failed.
 bool splitk_slot(hipStream_t st, float** partials, size_t* partial_floats, uint32_t** counters,
                  int* ncounters) {
-    static std::mutex mu;
-    static DevSlots devs[kMaxDev];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
-    std::lock_guard<std::mutex> lock(mu);
-    DevSlots& d = devs[dev];
+    std::lock_guard<std::mutex> lock(g_mu);
+    DevSlots& d = g_devs[dev];
     if (!d.resolved) {
         void* pa = nullptr;
         void* ca = nullptr;
@@ -67,19 +69,41 @@ bool splitk_slot(hipStream_t st, float** partials, size_t* partial_floats, uint3
         d.counters = reinterpret_cast<uint32_t*>(ca);
         d.resolved = true;
     }
-    int slot = -1;
-    for (int i = 0; i < d.nused; ++i)
-        if (d.owner[i] == st) slot = i;
+    int slot = -1, freed = -1;
+    for (int i = 0; i < d.nused; ++i) {
+        if (d.owner[i] == st && !d.released[i]) slot = i;
+        if (d.released[i] && freed < 0) freed = i;
+    }
     if (slot < 0) {
-        if (d.nused == xhip::kSplitSlots) return false;
-        slot = d.nused++;
+        if (freed >= 0) {
+            slot = freed;
+        } else {
+            if (d.nused == xhip::kSplitSlots) return false;
+            slot = d.nused++;
+        }
         d.owner[slot] = st;
+        d.released[slot] = false;
     }
     *partials = d.partials + (size_t)slot * xhip::kSplitPartialFloats;
     *partial_floats = xhip::kSplitPartialFloats;
     *counters = d.counters + (size_t)slot * xhip::kSplitCounters;
     *ncounters = xhip::kSplitCounters;
     return true;
+}
+
+
+// Gives the split-K slot of `st` on the current device back (its counters
+// are zero once the stream's work has finished).
+void splitk_release(hipStream_t st) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return;
+    std::lock_guard<std::mutex> lock(g_mu);
+    DevSlots& d = g_devs[dev];
+    for (int i = 0; i < d.nused; ++i)
+        if (d.owner[i] == st && !d.released[i]) {
+            d.released[i] = true;
+            d.owner[i] = nullptr;
+        }
 }
 
 }  // namespace xhip_host

@@ -193,3 +193,10 @@ def linear_int4_residual(residual: torch.Tensor, X, W_int4, scales, bias, M, N, 
     check("linear_int4_residual", L.xinfer_linear_int4_residual_f16(
         _stream(stream), _ptr(residual), _ptr(X), _ptr(W_int4), _ptr(scales), _ptr(bias), M, N, K,
         group_size))
+
+
+def stream_release(stream) -> None:
+    """Give back a stream's split-K slot and argmax scratch (no reference
+    counterpart; for callers that destroy streams)."""
+    L = load_library()
+    check("stream_release", L.xinfer_stream_release(_stream(stream)))
