@@ -206,6 +206,8 @@ def main():
     ap.add_argument("--quick", action="store_true", help="headline config only")
     ap.add_argument("--only", default="", help="comma list: cfg1,ns,cfg0,cfg2,fused,norm,layer,crc,cfg3,cfg4")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-exact", action="store_true",
+                    help="skip config 4 on the exact-dequant route (a child process)")
     ap.add_argument("--eager", action="store_true", help="time eager launches, not graph replay")
     ap.add_argument("--calib-copy", action="store_true",
                     help="run a plain 256 MiB device copy 20x (PMC calibration) and exit")
@@ -575,7 +577,7 @@ def run_suite(torch, dev, ops, synth, args, log, want, graph):
                            if exact_route else
                            "xhip::gemm_ws_int4_kernel (256x136 blocks; 4 MFMA waves copying their own X "
                            "rows, 4 weight-decode waves; B = fp16(q*s))")})
-        if not exact_route:
+        if not exact_route and not args.no_exact:
             # the same projection with the reference's dequantisation (exact
             # integer q, FP32 group scale) on the other GEMM kernel, in a
             # child process (the route is chosen from the environment once)
