@@ -151,11 +151,19 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     const int ngs = min(p.gps, ng - g0);
     const uint32_t row_bytes = (uint32_t)K >> 1;
 
-    // LDS: X slice as MFMA A operands [group][dword t][k-quarter][m < MR] (16 B
+    // LDS: X slice as MFMA A operands [group][k-quarter][dword t][m < MR] (16 B
     // each), then the block's results [wave of the run][row][m][e] (fp32:
     // one slice per wave sharing a run, summed in order), then the argmax
     // candidates of the waves (NW values, NW indices) and one flag word.
     f16x8* xs = reinterpret_cast<f16x8*>(smem);
+    // Slot of piece r (r = (group * 4 + k-quarter) * 4 + dword of the slice)
+    // of row m: row blocks of MR slots, the row XOR-swizzled by the
+    // k-quarter, so that the staging stores of consecutive pieces of one row
+    // spread over the 16-byte bank groups (conflict-free at MR = 4, 2-way at
+    // 8, 4-way at 16; 4 / 8 / 16-way unswizzled), while the A-operand reads
+    // of one piece by the MR rows stay one contiguous block and a lane's
+    // four dwords stay immediate offsets from one address.
+    auto xslot = [](int r, int m) { return r * MR + (m ^ ((r >> 2) & 3)); };
     float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * MR * 16);
     float* candv = outl + ((size_t)p.tiles_blk * 16 * M * E << p.lkw);
     int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
@@ -269,16 +277,56 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             const uint32_t xa[4] = {xv[t].x, xv[t].y, xv[t].z, xv[t].w};
             f16x2 pr[4];
             permute_x8(xa, pr);
-            xs[((gl * 4 + t) * 4 + cq) * MR + m] = pack_q8(pr);
+            xs[xslot((gl * 4 + cq) * 4 + t, m)] = pack_q8(pr);
         }
     };
+    // Without the norm the slice is staged by 16-byte pieces in row order:
+    // thread tid takes pieces tid + u NT, so consecutive lanes read
+    // consecutive 16 bytes of a row (whole 1 KB runs per load instruction;
+    // the chunk order below, rows fastest, put the lanes of a quad in
+    // different rows: measured ~3.5x slower per byte).  Piece r of row m
+    // (slice order) is dword t = r % 4 of k-quarter (r / 4) % 4 of group
+    // r / 16.  The norm form keeps the chunk order: a thread's chunks are
+    // then all of one row, which its row sums use.
+    constexpr bool norm = NORM != 0;  // p.norm_w set; NORM = 1: M == MR, 2: M < MR
+    const int ppr = ngs * 16;  // pieces per row of the slice
+    const int pieces = ppr * M;
+    const int dm = NT / ppr, dr = NT - dm * ppr;
+    struct PieceCursor { int m, r; };  // piece tid + u NT as (row, piece of the row)
+    auto advance = [&](PieceCursor& c) {
+        c.r += dr;
+        c.m += dm;
+        if (c.r >= ppr) {
+            c.r -= ppr;
+            ++c.m;
+        }
+    };
+    auto pget = [&](const PieceCursor& c) -> u32x4 {
+        return *reinterpret_cast<const u32x4*>(p.X + (size_t)c.m * K + (size_t)g0 * 128 + c.r * 8);
+    };
+    auto pput = [&](const PieceCursor& c, const u32x4 v) {
+        const uint32_t xa[4] = {v.x, v.y, v.z, v.w};
+        f16x2 pq[4];
+        permute_x8(xa, pq);
+        xs[xslot(c.r, c.m)] = pack_q8(pq);  // r = (gl * 4 + cq) * 4 + t
+    };
+    constexpr int kPU = 4 * kStageUnroll;  // pieces per thread and round (the chunks' registers)
     u32x4 xv0[kStageUnroll][4];
+    PieceCursor cl = {tid / ppr, tid - (tid / ppr) * ppr};  // load cursor
+    PieceCursor cs = cl;                                     // store cursor
+    if constexpr (!norm) {
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u)
-        if (tid + u * NT < chunks) get(tid + u * NT, xv0[u]);
+        for (int u = 0; u < kPU; ++u) {
+            if (tid + u * NT < pieces) xv0[u >> 2][u & 3] = pget(cl);
+            advance(cl);
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u)
+            if (tid + u * NT < chunks) get(tid + u * NT, xv0[u]);
+    }
     // RMSNorm weights: requested with X, stored to LDS once they land (the
     // host keeps K <= 6144: K / 4 <= kNormPT * NT)
-    constexpr bool norm = NORM != 0;  // p.norm_w set; NORM = 1: M == MR, 2: M < MR
     constexpr int kNormPT = 1536 / NT;
     float4 nwv[kNormPT];
 #pragma unroll
@@ -355,27 +403,46 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
         }
     }
 
+    if constexpr (!norm) {
 #pragma unroll
-    for (int u = 0; u < kStageUnroll; ++u)
-        if (tid + u * NT < chunks) {
-            if constexpr (norm) {
+        for (int u = 0; u < kPU; ++u) {
+            if (tid + u * NT < pieces) pput(cs, xv0[u >> 2][u & 3]);
+            advance(cs);
+        }
+        for (int i0 = tid + NT * kPU; i0 < pieces; i0 += NT * kPU) {  // further rounds
+            u32x4 xv[kPU];
+#pragma unroll
+            for (int u = 0; u < kPU; ++u) {
+                if (i0 + u * NT < pieces) xv[u] = pget(cl);
+                advance(cl);
+            }
+#pragma unroll
+            for (int u = 0; u < kPU; ++u) {
+                if (i0 + u * NT < pieces) pput(cs, xv[u]);
+                advance(cs);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u)
+            if (tid + u * NT < chunks) {
                 const int q = chunk_q(tid + u * NT);
                 float iv = inv;
                 if constexpr (NORM == 2) iv = rsum[chunk_m(tid + u * NT)];
                 const float4* wk = reinterpret_cast<const float4*>(nws + (g0 + (q >> 2)) * 128 + (q & 3) * 32);
 #pragma unroll
                 for (int t = 0; t < 4; ++t) xv0[u][t] = rms_apply8(xv0[u][t], wk[2 * t], wk[2 * t + 1], iv);
+                put(tid + u * NT, xv0[u]);
             }
-            put(tid + u * NT, xv0[u]);
+        for (int i0 = tid + NT * kStageUnroll; i0 < chunks; i0 += NT * kStageUnroll) {  // further rounds
+            u32x4 xv[kStageUnroll][4];
+#pragma unroll
+            for (int u = 0; u < kStageUnroll; ++u)
+                if (i0 + u * NT < chunks) get(i0 + u * NT, xv[u]);
+#pragma unroll
+            for (int u = 0; u < kStageUnroll; ++u)
+                if (i0 + u * NT < chunks) put(i0 + u * NT, xv[u]);
         }
-    for (int i0 = tid + NT * kStageUnroll; i0 < chunks; i0 += NT * kStageUnroll) {  // further rounds
-        u32x4 xv[kStageUnroll][4];
-#pragma unroll
-        for (int u = 0; u < kStageUnroll; ++u)
-            if (i0 + u * NT < chunks) get(i0 + u * NT, xv[u]);
-#pragma unroll
-        for (int u = 0; u < kStageUnroll; ++u)
-            if (i0 + u * NT < chunks) put(i0 + u * NT, xv[u]);
     }
     __syncthreads();  // X staged
 
@@ -387,7 +454,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // their results are never stored) of k-quarter l / 16; the stride of m
     // is the compile-time MR, so the four dwords of a group are immediate
     // offsets from one address.
-    const f16x8* xl = xs + kq * MR + (l16 < M ? l16 : M - 1);
+    const f16x8* xl = xs + xslot(kq * 4, l16 < M ? l16 : M - 1);
     auto compute_item = [&](int it, const MbItem<E>& b) {
         f16x8 xa[kGP][4];
         int gl[kGP];
@@ -396,7 +463,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             gl[gi] = it * kGP + gi;
             const f16x8* xg = xl + (gb + min(gl[gi], ngw - 1)) * (16 * MR);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) xa[gi][t] = xg[t * 4 * MR];
+            for (int t = 0; t < 4; ++t) xa[gi][t] = xg[t * MR];
         }
 #pragma unroll
         for (int x = 0; x < E; ++x) {
