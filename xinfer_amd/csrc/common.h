@@ -187,6 +187,70 @@ __device__ __forceinline__ float argmax_key(float v, int64_t idx) {
 __device__ __forceinline__ bool arg_better(float av, int32_t ai, float bv, int32_t bi) {
     return av > bv || (av == bv && ai < bi);
 }
+
+// Argmax candidates of 8 rows over the 64 lanes in one pass, the pattern of
+// wave_sum_multi with arg_better in place of the sum: three halving steps
+// on lane bits 0-2 leave lane L with a partial candidate of row L mod 8,
+// then a row rotation by 8 and the 16 / 32 swaps combine lanes of the same
+// row.  Lane L returns row L mod 8's candidate (a total order, so the
+// result does not depend on the order of the combines).
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i(int32_t v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+__device__ __forceinline__ void swap32_pair(float& v, int32_t& i) {
+    float tv = v;
+    int32_t ti = i;
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(v), "+v"(tv));
+    asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(i), "+v"(ti));
+    if (arg_better(tv, ti, v, i)) { v = tv; i = ti; }
+}
+__device__ __forceinline__ void swap16_pair(float& v, int32_t& i) {
+    float tv = v;
+    int32_t ti = i;
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(v), "+v"(tv));
+    asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(i), "+v"(ti));
+    if (arg_better(tv, ti, v, i)) { v = tv; i = ti; }
+}
+__device__ __forceinline__ void wave_argmax_multi8(const float (&bv)[8], const int32_t (&bi)[8], int lane,
+                                                   float& rv, int32_t& ri) {
+    float a[8];
+    int32_t b[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        a[j] = bv[j];
+        b[j] = bi[j];
+    }
+    auto halve = [&](auto ctrl, int n, bool bit) {
+        constexpr int C = decltype(ctrl)::value;
+#pragma unroll
+        for (int j = 0; j < n / 2; ++j) {
+            const float kv = bit ? a[2 * j + 1] : a[2 * j];
+            const int32_t ki = bit ? b[2 * j + 1] : b[2 * j];
+            const float sv = bit ? a[2 * j] : a[2 * j + 1];
+            const int32_t si = bit ? b[2 * j] : b[2 * j + 1];
+            const float ov = dpp<C>(sv);
+            const int32_t oi = dpp_i<C>(si);
+            const bool t = arg_better(ov, oi, kv, ki);
+            a[j] = t ? ov : kv;
+            b[j] = t ? oi : ki;
+        }
+    };
+    halve(std::integral_constant<int, 0xB1>{}, 8, (lane & 1) != 0);
+    halve(std::integral_constant<int, 0x4E>{}, 4, (lane & 2) != 0);
+    halve(std::integral_constant<int, 0x124>{}, 2, (lane & 4) != 0);
+    float v = a[0];
+    int32_t i = b[0];
+    {
+        const float ov = dpp<0x128>(v);
+        const int32_t oi = dpp_i<0x128>(i);
+        if (arg_better(ov, oi, v, i)) { v = ov; i = oi; }
+    }
+    swap16_pair(v, i);
+    swap32_pair(v, i);
+    rv = v;
+    ri = i;
+}
 // Per-row RMSNorm factors of X [M][K] (M <= 8, K a multiple of 8) for a
 // block of NTHREADS threads: inv[m] = 1 / sqrt(sum_k x^2 / K + eps), the FP32
 // sum of src/ops/rmsnorm.cpp:45-71 (summed in a fixed order here, so every

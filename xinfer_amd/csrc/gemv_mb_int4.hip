@@ -165,11 +165,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // four dwords stay immediate offsets from one address.
     auto xslot = [](int r, int m) { return r * MR + (m ^ ((r >> 2) & 3)); };
     float* outl = reinterpret_cast<float*>(smem + (size_t)p.gps * 16 * MR * 16);
+    // (argmax: 8 candidates per wave, one per activation row)
+    constexpr int kCand = EPI == MB_ARGMAX ? 8 : 1;
     float* candv = outl + ((size_t)p.tiles_blk * 16 * M * E << p.lkw);
-    int32_t* candi = reinterpret_cast<int32_t*>(candv + NW);
-    int32_t* flag = candi + NW;
+    int32_t* candi = reinterpret_cast<int32_t*>(candv + NW * kCand);
+    int32_t* flag = candi + NW * kCand;
     // RMSNorm (norm_w set): the weights [K] and the waves' row sums [NW][MR]
-    float* nws = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(candv) + 2 * NW * 4 + 16);
+    float* nws = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(candv) + 2 * NW * kCand * 4 + 16);
     float* rsum = nws + K;
 
     // Waves come in runs of kw = 2^lkw: the waves of a run share its tiles
@@ -201,15 +203,21 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // and are never stored), the group offset is wave-uniform (the buffer
     // instruction's scalar offset), and a padding group past the wave's
     // last reloads that last group and gets a zero scale in the compute.
-    uint32_t vw = 0, vs = 0;  // lane offsets (bytes) of the load tile's row at the wave's first group
+    uint32_t vwt = 0, vst = 0;  // lane offsets (bytes) of the load tile's row at the wave's first group
     auto set_tile = [&](int tile) {
         const uint32_t n = (uint32_t)min(n0 + tile * 16 + l16, N - 1);
-        vw = n * row_bytes + (uint32_t)(g0 + gb) * 64u + (uint32_t)kq * 16u;
-        vs = (n * (uint32_t)ng + (uint32_t)(g0 + gb)) * 2u;
+        vwt = n * row_bytes + (uint32_t)(g0 + gb) * 64u + (uint32_t)kq * 16u;
+        vst = (n * (uint32_t)ng + (uint32_t)(g0 + gb)) * 2u;
     };
     set_tile(t0);
     int lt = t0, lg = 0, lrem = nreal;  // load cursor (wave-uniform): tile, item, items left
     auto load_next = [&](MbItem<E>& b) {
+        // argmax: past the wave's last item, out-of-range offsets (zeros
+        // without memory traffic, nothing for the epilogue's waits to wait
+        // on; the other epilogues measured faster repeating the last item)
+        const bool oor = EPI == MB_ARGMAX && lrem <= 0;
+        const uint32_t vw = oor ? kOutOfRange : vwt;
+        const uint32_t vs = oor ? kOutOfRange : vst;
         if constexpr (E == 2) {
             // SwiGLU: a matrix's two groups (the two halves of each row's
             // 128-byte line) back to back, then the other matrix's (gate/up
@@ -301,24 +309,41 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             ++c.m;
         }
     };
-    auto pget = [&](const PieceCursor& c) -> u32x4 {
-        return *reinterpret_cast<const u32x4*>(p.X + (size_t)c.m * K + (size_t)g0 * 128 + c.r * 8);
-    };
     auto pput = [&](const PieceCursor& c, const u32x4 v) {
         const uint32_t xa[4] = {v.x, v.y, v.z, v.w};
         f16x2 pq[4];
         permute_x8(xa, pq);
         xs[xslot(c.r, c.m)] = pack_q8(pq);  // r = (gl * 4 + cq) * 4 + t
     };
+    // X through a buffer resource: 32-bit offsets, and a piece past the
+    // slice reads zeros without a branch around its load
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)p.X, (short)0, (int)((uint32_t)M * (uint32_t)K * 2u), 0x00020000);
+    auto poff = [&](const PieceCursor& c) -> uint32_t {
+        return ((uint32_t)c.m * (uint32_t)K + (uint32_t)g0 * 128u + (uint32_t)c.r * 8u) * 2u;
+    };
+    // the slice is all of X (one k-slice): piece i is bytes 16 i .. 16 i + 15
+    // (the LM head; the other epilogues measured no faster with this form)
+    const bool whole = EPI == MB_ARGMAX && ngs * 128 == K;
+    const int nround = __builtin_amdgcn_readfirstlane((pieces + NT - 1) / NT);
     constexpr int kPU = 4 * kStageUnroll;  // pieces per thread and round (the chunks' registers)
     u32x4 xv0[kStageUnroll][4];
     PieceCursor cl = {tid / ppr, tid - (tid / ppr) * ppr};  // load cursor
     PieceCursor cs = cl;                                     // store cursor
     if constexpr (!norm) {
+        if (whole) {
 #pragma unroll
-        for (int u = 0; u < kPU; ++u) {
-            if (tid + u * NT < pieces) xv0[u >> 2][u & 3] = pget(cl);
-            advance(cl);
+            for (int u = 0; u < kPU; ++u)
+                if (u < nround)
+                    xv0[u >> 2][u & 3] = __builtin_amdgcn_raw_buffer_load_b128(rx, (int)(tid * 16), u * NT * 16, 0);
+        } else {
+#pragma unroll
+            for (int u = 0; u < kPU; ++u) {
+                if (tid + u * NT < pieces)
+                    xv0[u >> 2][u & 3] = *reinterpret_cast<const u32x4*>(
+                        p.X + (size_t)cl.m * K + (size_t)g0 * 128 + cl.r * 8);
+                advance(cl);
+            }
         }
     } else {
 #pragma unroll
@@ -409,11 +434,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             if (tid + u * NT < pieces) pput(cs, xv0[u >> 2][u & 3]);
             advance(cs);
         }
+        cl = cs;  // piece tid + kPU NT
         for (int i0 = tid + NT * kPU; i0 < pieces; i0 += NT * kPU) {  // further rounds
             u32x4 xv[kPU];
 #pragma unroll
             for (int u = 0; u < kPU; ++u) {
-                if (i0 + u * NT < pieces) xv[u] = pget(cl);
+                xv[u] = __builtin_amdgcn_raw_buffer_load_b128(
+                    rx, (int)(i0 + u * NT < pieces ? poff(cl) : kOutOfRange), 0, 0);
                 advance(cl);
             }
 #pragma unroll
@@ -591,40 +618,69 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
         if (tid == 0) __hip_atomic_store(&p.cnt[grange], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    if (EPI == MB_ARGMAX) {
-        for (int m = 0; m < M; ++m) {
-            float bv = -__builtin_inff();
-            int32_t bi = 0x7FFFFFFF;
-            for (int rl = tid; rl < rows_here; rl += NT) {
-                const int n = n0 + rl;
-                float v = outl[rl * M + m];
-                if (d.bias) v += d.bias[n];
-                if (d.Y) reinterpret_cast<float*>(d.Y)[(size_t)m * N + n] = v;
-                const float key = argmax_key(v, n);
-                if (arg_better(key, n, bv, bi)) { bv = key; bi = n; }
+    if constexpr (EPI == MB_ARGMAX) {
+        // Every activation row at once: a thread's rows, then the wave in
+        // one multi-row pass (DPP halving steps and lane swaps: lane L ends
+        // with row L mod 8), then the waves for row m by thread m.
+        // arg_better is a total order (value, then the lower index), so the
+        // candidate does not depend on the order of the comparisons.  (One
+        // row at a time, with shuffles and two barriers per row, this
+        // epilogue cost ~5 us of the M = 8 LM head.)
+        float bv[kCand];
+        int32_t bi[kCand];
+#pragma unroll
+        for (int m = 0; m < kCand; ++m) {
+            bv[m] = -__builtin_inff();
+            bi[m] = 0x7FFFFFFF;
+        }
+        // the descriptor's pointers once (a store through Y could otherwise
+        // make the compiler reload them from the kernel arguments)
+        const float* const biasp = d.bias;
+        float* const logits = reinterpret_cast<float*>(d.Y);
+        for (int rl = tid; rl < rows_here; rl += NT) {
+            const int n = n0 + rl;
+            const float bn = biasp ? biasp[n] : 0.0f;
+            float v[kCand];
+            if (M == 8) {  // the row's M results: two 16-byte LDS reads
+                const float4 a = reinterpret_cast<const float4*>(outl + rl * 8)[0];
+                const float4 b2 = reinterpret_cast<const float4*>(outl + rl * 8)[1];
+                v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+                v[4] = b2.x; v[5] = b2.y; v[6] = b2.z; v[7] = b2.w;
+            } else {
+#pragma unroll
+                for (int m = 0; m < kCand; ++m) v[m] = m < M ? outl[rl * M + m] : 0.0f;
             }
 #pragma unroll
-            for (int off = 32; off > 0; off >>= 1) {
-                const float ov = __shfl_xor(bv, off);
-                const int32_t oi = __shfl_xor(bi, off);
-                if (arg_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+            for (int m = 0; m < kCand; ++m) {
+                if (m < M) {
+                    const float vm = biasp ? v[m] + bn : v[m];
+                    if (logits) logits[(size_t)m * N + n] = vm;
+                    const float key = argmax_key(vm, n);
+                    if (arg_better(key, n, bv[m], bi[m])) { bv[m] = key; bi[m] = n; }
+                }
             }
-            if (lane == 0) {
-                candv[wave] = bv;
-                candi[wave] = bi;
-            }
-            __syncthreads();
-            if (tid == 0) {
-                float b = candv[0];
-                int32_t i = candi[0];
-                for (int w = 1; w < NW; ++w)
-                    if (arg_better(candv[w], candi[w], b, i)) { b = candv[w]; i = candi[w]; }
-                ArgCand c;
-                c.v = b;
-                c.i = i;
-                p.parts[(size_t)m * p.nranges + grange] = c;
-            }
-            __syncthreads();
+        }
+        // lane L: the wave's candidate of row L mod 8
+        float rv;
+        int32_t ri;
+        wave_argmax_multi8(bv, bi, lane, rv, ri);
+        if (lane < kCand) {
+            candv[wave * kCand + lane] = rv;
+            candi[wave * kCand + lane] = ri;
+        }
+        __syncthreads();
+        if (tid < M) {
+            float b = candv[tid];
+            int32_t i = candi[tid];
+            for (int w = 1; w < NW; ++w)
+                if (arg_better(candv[w * kCand + tid], candi[w * kCand + tid], b, i)) {
+                    b = candv[w * kCand + tid];
+                    i = candi[w * kCand + tid];
+                }
+            ArgCand c;
+            c.v = b;
+            c.i = i;
+            p.parts[(size_t)tid * p.nranges + grange] = c;
         }
     } else {
         for (int o = tid; o < nout; o += NT) {
@@ -880,7 +936,7 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
             }
             for (int kwc = 1; kwc <= kw_cap; kwc *= 2) {
                 if (tmin < nw / kwc) continue;  // a run of waves without a tile
-                const size_t l = (size_t)gps * xg + (size_t)tmax * 16 * M * E * 4 * kwc + 2 * nw * 4 + 16 + norm_lds;
+                const size_t l = (size_t)gps * xg + (size_t)tmax * 16 * M * E * 4 * kwc + 2 * nw * 4 * (EPI == MB_ARGMAX ? 8 : 1) + 16 + norm_lds;
                 if (l * c > kMaxLds) continue;
                 const int64_t cc = cost(used * ks, tmax, kwc);
                 if (cc < best) {
@@ -895,7 +951,7 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     }
     int lkw = 0;
     while ((1 << lkw) < kw) ++lkw;
-    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 + 16 + norm_lds;
+    const size_t lds = (size_t)gps * xg + (size_t)tiles_blk * 16 * M * E * 4 * kw + 2 * nw * 4 * (EPI == MB_ARGMAX ? 8 : 1) + 16 + norm_lds;
     if (lds > kMaxLds) return false;
     // the norm's single staging round: chunks and weights per thread within
     // the kernel's unrolls (8 / 4 chunks at 4 / 8 waves, 1536 float4 of
