@@ -101,10 +101,11 @@ constexpr int kGP = XHIP_MB_GP;  // 128-k groups per item
 // loads do not hit stale lines of another XCD's L2.
 constexpr int kDeviceCoherent = 16;
 
+static_assert(kGP == 2, "an item's two group scales are one dword");
 template <int E>
 struct MbItem {
     u32x4 w[E * kGP];
-    uint32_t s[E * kGP];  // raw fp16 scale bits, converted at use
+    uint32_t s[E * kGP];  // fp16 group scales: s[x] holds both of matrix x's (the LM head: one per s[gi])
 };
 
 __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
@@ -190,7 +191,13 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     const int nreal = (t1 - t0) * nig;
 
     const int nrec_w = (int)((uint32_t)N * row_bytes);
-    const int nrec_s = (int)((uint32_t)N * (uint32_t)ng * 2u);
+    // Scales: one 4-byte load per item and lane holds both groups' fp16
+    // scales (a dword load at any 2-byte offset; two 2-byte loads per item,
+    // scattered over the 16 rows, cost a pure read of this weight pattern
+    // ~25 % of its rate, the dword ~6 %).  The resource reaches 2 bytes past
+    // the array, inside its allocation's granule, so the dword holding the
+    // last scale reads it (its second half is a padding group's, unused).
+    const int nrec_s = (int)((uint32_t)N * (uint32_t)ng * 2u + 2u);
     const __amdgpu_buffer_rsrc_t rw0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.W, (short)0, nrec_w, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.S, (short)0, nrec_s, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -227,23 +234,25 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             for (int e = 0; e < E; ++e) {
 #pragma unroll
                 for (int gi = 0; gi < kGP; ++gi) {
-                    const int g = min(lg * kGP + gi, ngw - 1);
+                    const int g = __builtin_amdgcn_readfirstlane(min(lg * kGP + gi, ngw - 1));  // wave-uniform: a scalar offset
                     b.w[e * kGP + gi] =
                         __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)vw, g * 64, XHIP_MB_AUX);
                 }
-#pragma unroll
-                for (int gi = 0; gi < kGP; ++gi) {
-                    const int g = min(lg * kGP + gi, ngw - 1);
-                    b.s[e * kGP + gi] = __builtin_amdgcn_raw_buffer_load_b16(e ? rs1 : rs0, (int)vs, g * 2, 0);
-                }
+                b.s[e] = __builtin_amdgcn_raw_buffer_load_b32(e ? rs1 : rs0, (int)vs, __builtin_amdgcn_readfirstlane(lg * (2 * kGP)), 0);
             }
         } else {
 #pragma unroll
             for (int gi = 0; gi < kGP; ++gi) {
-                const int g = min(lg * kGP + gi, ngw - 1);
+                // wave-uniform (a scalar offset; without the explicit form
+                // the compiler waterfalled some plain instantiations)
+                const int g = EPI == MB_ARGMAX ? min(lg * kGP + gi, ngw - 1)
+                                               : __builtin_amdgcn_readfirstlane(min(lg * kGP + gi, ngw - 1));
                 b.w[gi] = __builtin_amdgcn_raw_buffer_load_b128(rw0, (int)vw, g * 64, XHIP_MB_AUX);
-                b.s[gi] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vs, g * 2, 0);
+                if constexpr (EPI == MB_ARGMAX)  // the LM head measured faster with a 2-byte load per group
+                    b.s[gi] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vs, g * 2, 0);
             }
+            if constexpr (EPI != MB_ARGMAX)
+                b.s[0] = __builtin_amdgcn_raw_buffer_load_b32(rs0, (int)vs, __builtin_amdgcn_readfirstlane(lg * (2 * kGP)), 0);
         }
         // past the last item the cursor stays: the extra loads repeat it
         if (--lrem > 0 && ++lg == nig) {
@@ -511,7 +520,8 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             }
 #pragma unroll
             for (int gi = 0; gi < kGP; ++gi) {
-                const float s = gl[gi] < ngw ? h2f((uint16_t)b.s[x * kGP + gi]) : 0.0f;
+                const uint16_t sb = EPI == MB_ARGMAX ? (uint16_t)b.s[gi] : (uint16_t)(b.s[x] >> (16 * gi));
+                const float s = gl[gi] < ngw ? h2f(sb) : 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[x][e] = __builtin_fmaf(s, c[gi][e], acc[x][e]);
             }
