@@ -212,6 +212,22 @@ __device__ __forceinline__ void swap16_pair(float& v, int32_t& i) {
     asm("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(i), "+v"(ti));
     if (arg_better(tv, ti, v, i)) { v = tv; i = ti; }
 }
+// One argmax candidate over the 64 lanes (every lane receives the result):
+// quad exchanges, row rotations by 4 and 8, then the 16 / 32 swaps.
+__device__ __forceinline__ void wave_argmax1(float& v, int32_t& i) {
+    auto step = [&](auto ctrl) {
+        constexpr int C = decltype(ctrl)::value;
+        const float ov = dpp<C>(v);
+        const int32_t oi = dpp_i<C>(i);
+        if (arg_better(ov, oi, v, i)) { v = ov; i = oi; }
+    };
+    step(std::integral_constant<int, 0xB1>{});
+    step(std::integral_constant<int, 0x4E>{});
+    step(std::integral_constant<int, 0x124>{});
+    step(std::integral_constant<int, 0x128>{});
+    swap16_pair(v, i);
+    swap32_pair(v, i);
+}
 __device__ __forceinline__ void wave_argmax_multi8(const float (&bv)[8], const int32_t (&bi)[8], int lane,
                                                    float& rv, int32_t& ri) {
     float a[8];

@@ -478,21 +478,22 @@ __global__ __launch_bounds__(256) void argmax_finalize_kernel(const ArgCand* par
         const ArgCand c = pm[i];
         if (arg_better(c.v, c.i, bv, bi)) { bv = c.v; bi = c.i; }
     }
-    __shared__ float sv[256];
-    __shared__ int32_t si[256];
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
+    // the wave by lane exchanges, then the 4 waves in order (a total
+    // order: the result does not depend on the combine order)
+    wave_argmax1(bv, bi);
+    __shared__ float sv[4];
+    __shared__ int32_t si[4];
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-            const float ov = sv[threadIdx.x + s];
-            const int32_t oi = si[threadIdx.x + s];
-            if (arg_better(ov, oi, sv[threadIdx.x], si[threadIdx.x])) {
-                sv[threadIdx.x] = ov;
-                si[threadIdx.x] = oi;
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (arg_better(sv[w], si[w], sv[0], si[0])) {
+                sv[0] = sv[w];
+                si[0] = si[w];
             }
-        }
-        __syncthreads();
     }
     if (threadIdx.x == 0) ids[m] = (IdT)(si[0] == 0x7FFFFFFF ? 0 : si[0]);
 }
