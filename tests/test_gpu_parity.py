@@ -367,6 +367,14 @@ def test_cfg4_prefill_m512_sampled_rows():
     print(_linear_case(512, 17408, 5120, sample_rows=[0, 1, 77, 255, 256, 300, 510, 511]))
 
 
+def test_cfg4_prefill_m512_full_row_tile():
+    """Config 4 on the prefill GEMM (fp16 output, B = fp16(q*s)): every
+    output of the first 256-row block of M (one full row tile across all
+    17408 columns, i.e. 128 column tiles) plus the first and last rows of
+    the second, against the double-accumulate oracle."""
+    print(_linear_case(512, 17408, 5120, sample_rows=list(range(256)) + [256, 383, 511]))
+
+
 # --------------------------------------------------------- argmax edges ----
 
 def test_argmax_edges():
