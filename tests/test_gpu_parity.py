@@ -485,6 +485,30 @@ def test_prefill_swiglu(M, N, K):
     print(check_f16_tol(to_np(Y)[rows], ref))
 
 
+@pytest.mark.parametrize("out", ["f16", "f32"])
+@pytest.mark.parametrize("M,N,K", [(4, 33, 384), (8, 17, 640), (5, 31, 1152), (3, 9, 384)])
+def test_small_batch_odd_groups_last_scale(M, N, K, out):
+    """Small-batch shapes whose waves hold an odd number of 128-k groups:
+    each row's last item pairs a real group with a padding group, and the
+    scale array's last scale comes through the clamped 4-byte load (the
+    dword read 2 bytes lower, its upper half used)."""
+    print(_linear_case(M, N, K, seed=N, out=out))
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 33, 384), (8, 17, 640)])
+def test_small_batch_swiglu_odd_groups(M, N, K):
+    import torch
+    ops = _ops()
+    Wg, Wu = synth.packed_weights(2, N, K), synth.packed_weights(2, N, K, synth.STREAM_W2)
+    Sg, Su = synth.scales(2, N, K), synth.scales(2, N, K, stream=synth.STREAM_S2)
+    Xb = synth.activations(2, M, K)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), to_dev(Wg), f16_dev(Sg), to_dev(Wu), f16_dev(Su),
+                                M, N, K)
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb), Wg, Sg, Wu, Su, M, N, K, nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y), ref))
+
+
 def test_prefill_fused_descs_m64():
     import torch
     ops = _ops()

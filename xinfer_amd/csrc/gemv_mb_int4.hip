@@ -106,6 +106,7 @@ template <int E>
 struct MbItem {
     u32x4 w[E * kGP];
     uint32_t s[E * kGP];  // fp16 group scales: s[x] holds both of matrix x's (the LM head: one per s[gi])
+    uint32_t sh[E];       // s[x]'s first scale at bit sh[x] (0, or 16 for the array's last scale)
 };
 
 __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
@@ -194,10 +195,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // Scales: one 4-byte load per item and lane holds both groups' fp16
     // scales (a dword load at any 2-byte offset; two 2-byte loads per item,
     // scattered over the 16 rows, cost a pure read of this weight pattern
-    // ~25 % of its rate, the dword ~6 %).  The resource reaches 2 bytes past
-    // the array, inside its allocation's granule, so the dword holding the
-    // last scale reads it (its second half is a padding group's, unused).
-    const int nrec_s = (int)((uint32_t)N * (uint32_t)ng * 2u + 2u);
+    // ~25 % of its rate, the dword ~6 %).  No load reaches past the scale
+    // array: the one dword that would (the array's last scale, in an item
+    // whose second group is padding) is read 2 bytes lower and its upper
+    // half used.
+    const int nrec_s = (int)((uint32_t)N * (uint32_t)ng * 2u);
+    const uint32_t slast = (uint32_t)nrec_s - 4u;  // the host keeps N K / 128 >= 2
     const __amdgpu_buffer_rsrc_t rw0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.W, (short)0, nrec_w, 0x00020000);
     const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc((void*)d.S, (short)0, nrec_s, 0x00020000);
     const __amdgpu_buffer_rsrc_t rw1 = __builtin_amdgcn_make_buffer_rsrc(
@@ -218,6 +221,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     };
     set_tile(t0);
     int lt = t0, lg = 0, lrem = nreal;  // load cursor (wave-uniform): tile, item, items left
+    // the item's two group scales; sh = 16 where the dword was read 2 bytes
+    // lower (its upper half is the first group's scale)
+    auto load_scales = [&](const __amdgpu_buffer_rsrc_t& rs, uint32_t vs, uint32_t& sh) -> uint32_t {
+        const uint32_t o = vs + (uint32_t)(lg * (2 * kGP));
+        const uint32_t oc = o < slast ? o : slast;
+        sh = (o - oc) << 3;
+        return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)oc, 0, 0);
+    };
     auto load_next = [&](MbItem<E>& b) {
         // argmax: past the wave's last item, out-of-range offsets (zeros
         // without memory traffic, nothing for the epilogue's waits to wait
@@ -238,7 +249,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
                     b.w[e * kGP + gi] =
                         __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)vw, g * 64, XHIP_MB_AUX);
                 }
-                b.s[e] = __builtin_amdgcn_raw_buffer_load_b32(e ? rs1 : rs0, (int)vs, __builtin_amdgcn_readfirstlane(lg * (2 * kGP)), 0);
+                b.s[e] = load_scales(e ? rs1 : rs0, vs, b.sh[e]);
             }
         } else {
 #pragma unroll
@@ -251,8 +262,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
                 if constexpr (EPI == MB_ARGMAX)  // the LM head measured faster with a 2-byte load per group
                     b.s[gi] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vs, g * 2, 0);
             }
-            if constexpr (EPI != MB_ARGMAX)
-                b.s[0] = __builtin_amdgcn_raw_buffer_load_b32(rs0, (int)vs, __builtin_amdgcn_readfirstlane(lg * (2 * kGP)), 0);
+            if constexpr (EPI != MB_ARGMAX) b.s[0] = load_scales(rs0, vs, b.sh[0]);
         }
         // past the last item the cursor stays: the extra loads repeat it
         if (--lrem > 0 && ++lg == nig) {
@@ -520,7 +530,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
             }
 #pragma unroll
             for (int gi = 0; gi < kGP; ++gi) {
-                const uint16_t sb = EPI == MB_ARGMAX ? (uint16_t)b.s[gi] : (uint16_t)(b.s[x] >> (16 * gi));
+                const uint16_t sb = EPI == MB_ARGMAX ? (uint16_t)b.s[gi] : (uint16_t)((b.s[x] >> b.sh[x]) >> (16 * gi));
                 const float s = gl[gi] < ngw ? h2f(sb) : 0.0f;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[x][e] = __builtin_fmaf(s, c[gi][e], acc[x][e]);
@@ -816,6 +826,8 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     // global-X path is slower than this kernel (K = 17408: 20.3 vs 14.5 us)
     const int min_m = ov.min_m > 0 ? ov.min_m : gemv_stages_x(2, p.K) ? 3 : 2;
     if (M < min_m || M < 2 || M > (EPI == MB_ARGMAX ? 8 : kMaxMbM)) return false;
+    for (int i = 0; i < p.ndesc; ++i)  // the kernel's 4-byte scale loads need two scales
+        if ((int64_t)p.d[i].N * (p.K / 128) < 2) return false;
     const int E = EPI == MB_SWIGLU ? 2 : 1;
     const int ng = p.K / 128;
     const int cus = num_cus();
