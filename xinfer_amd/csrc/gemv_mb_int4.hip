@@ -384,8 +384,9 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // items in flight per wave: a SwiGLU item carries both matrices' groups
     // (twice the bytes), and one item less measured faster there (gate/up
     // M = 4 / 8 28.9 / 31.4 -> 28.2 / 30.3 us) while the plain and argmax
-    // forms lost 1.5-4.6 % with it
-    constexpr int PF = EPI == MB_SWIGLU ? XHIP_MB_PF - 1 : XHIP_MB_PF;
+    // forms lost 1.5-4.6 % with it; the LM head (186 items a wave) gains
+    // from one more (M = 8 84.5 -> 83.3 us; the plain form lost with it)
+    constexpr int PF = EPI == MB_SWIGLU ? XHIP_MB_PF - 1 : EPI == MB_ARGMAX ? XHIP_MB_PF + 1 : XHIP_MB_PF;
     MbItem<E> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
@@ -868,8 +869,10 @@ bool plan_mb(MbParams& p, MbPlan& pl, size_t ws_cap, int64_t cnt_cap, bool raise
     if (ks > ng) ks = ng;
     const size_t slice = (size_t)ng * xg / ks;
     // X slice beyond nw_at: 8 waves.  The LM head keeps 4 waves at one block
-    // per CU (M = 8, N = 151936: 94.0 -> 89.5 us against 8 waves).
-    const size_t nw_at = (long_k8 || whole8) ? 96 * 1024 : 64 * 1024;
+    // per CU (M = 8, N = 151936: 94.0 -> 89.5 us against 8 waves).  Long K at
+    // the 8-row stride (config 2 at M = 5-8) takes 8 waves for its 92 KB
+    // slices (M = 8 19.3 -> 18.4 us).
+    const size_t nw_at = long_k8 ? 64 * 1024 : whole8 ? 96 * 1024 : 64 * 1024;
     int nw = ov.nw > 0 ? ov.nw : (EPI != MB_ARGMAX && slice > nw_at) ? 8 : 4;
     nw = nw >= 16 ? 16 : nw >= 8 ? 8 : 4;
     int bpc = ov.bpc > 0 ? ov.bpc : (nw >= 8 ? 1 : 2);
