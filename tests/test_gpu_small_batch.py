@@ -164,6 +164,31 @@ def test_small_batch_lm_head_argmax(M):
     _check_f32(lg, ref)
 
 
+@pytest.mark.parametrize("M,N,K", [(3, 1001, 640), (8, 4099, 1152), (5, 33, 384), (2, 17, 128)])
+def test_small_batch_lm_head_odd_groups_ragged_rows(M, N, K):
+    """LM head with odd group counts (a wave's last item has a padding
+    group) and N not a multiple of 16 (the last tile's rows clamped), the
+    winner planted in the last row: every logit and every id."""
+    import torch
+    ops = _ops()
+    W, S, Xb = _inputs(60 + M, M, N, K, 0.01)
+    # row N-1 = sign(X[0]) (quantized): the largest logit of row 0 at least
+    Wq, Sq = oracle.quantize_int4(np.sign(oracle.f16_to_f32(Xb)[0])[None, :].astype(np.float32) * 0.3)
+    W[N - 1], S[N - 1] = Wq[0], Sq[0]
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K)
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    logits = _empty((M, N), torch.float32)
+    ops.lm_head_argmax_int4(ids, logits, f16_dev(Xb), to_dev(W), f16_dev(S), M, N, K)
+    got, lg = to_np(ids), to_np(logits)
+    _check_f32(lg, ref)
+    for m in range(M):
+        print("row", m, "id", got[m], "margin", oracle.top2_margin(ref[m]))
+        assert got[m] == oracle.argmax(lg[m])
+        if oracle.top2_margin(ref[m]) > 1e-3:
+            assert got[m] == oracle.argmax(ref[m])
+    assert got[0] == N - 1
+
+
 def test_small_batch_lm_head_ties_lowest_index():
     import torch
     ops = _ops()
