@@ -164,11 +164,14 @@ def test_small_batch_lm_head_argmax(M):
     _check_f32(lg, ref)
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 1001, 640), (8, 4099, 1152), (5, 33, 384), (2, 17, 128)])
+@pytest.mark.parametrize("M,N,K", [(3, 1001, 640), (8, 4099, 1152), (5, 33, 384), (2, 17, 128),
+                                   (4, 3001, 17408), (8, 1000, 9216)])
 def test_small_batch_lm_head_odd_groups_ragged_rows(M, N, K):
     """LM head with odd group counts (a wave's last item has a padding
     group) and N not a multiple of 16 (the last tile's rows clamped), the
-    winner planted in the last row: every logit and every id."""
+    winner planted in the last row: every logit and every id.  The last two
+    shapes stage X in two rounds (the biased decode's bias terms summed in
+    both)."""
     import torch
     ops = _ops()
     W, S, Xb = _inputs(60 + M, M, N, K, 0.01)
@@ -187,6 +190,49 @@ def test_small_batch_lm_head_odd_groups_ragged_rows(M, N, K):
         if oracle.top2_margin(ref[m]) > 1e-3:
             assert got[m] == oracle.argmax(ref[m])
     assert got[0] == N - 1
+
+
+@pytest.mark.parametrize("M,dc", [(8, 1.0), (4, -2.0), (8, 4.0), (1, 4.0), (1, -1.0)])
+def test_small_batch_lm_head_dc_offset_activations(M, dc):
+    """Activations with a large common offset (every x near dc): the FP32
+    logits stay within the reference's 1e-4 bound and the ids match."""
+    import torch
+    ops = _ops()
+    N, K = 4096, 5120
+    W, S, _ = _inputs(90 + M, M, N, K, 0.01)
+    rng = np.random.default_rng(90 + M)
+    Xb = (dc + 0.05 * rng.standard_normal((M, K))).astype(np.float16).view(np.uint16)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+    ids = torch.full((M,), -1, dtype=torch.int32, device="cuda")
+    logits = _empty((M, N), torch.float32)
+    ops.lm_head_argmax_int4(ids, logits, f16_dev(Xb), to_dev(W), f16_dev(S), M, N, K)
+    got, lg = to_np(ids), to_np(logits)
+    err = np.abs(lg - ref).max()
+    print("max err", err, "bound", 1e-4 * max(1.0, np.abs(ref).max()), "rel_l2", kat.rel_l2(lg, ref))
+    _check_f32(lg, ref)
+    for m in range(M):
+        assert got[m] == oracle.argmax(lg[m])
+        if oracle.top2_margin(ref[m]) > 1e-3:
+            assert got[m] == oracle.argmax(ref[m])
+
+
+@pytest.mark.parametrize("M,N,K,dc", [(1, 4096, 5120, 4.0), (1, 4096, 17408, 2.0), (2, 4096, 5120, 4.0),
+                                      (4, 2048, 6144, -3.0), (8, 2048, 5120, 4.0), (1, 48, 5120, 4.0)])
+def test_linear_fp32_dc_offset_activations(M, N, K, dc):
+    """fp32 outputs with activations near a common offset (the decode's
+    folded bias terms grow with it) on every M = 1..8 route: within the
+    reference's 1e-4 bound."""
+    import torch
+    ops = _ops()
+    W, S, _ = _inputs(70 + M, M, N, K, 0.01)
+    rng = np.random.default_rng(70 + M)
+    Xb = (dc + 0.05 * rng.standard_normal((M, K))).astype(np.float16).view(np.uint16)
+    ref = oracle.linear_int4(oracle.f16_to_f32(Xb), W, S, M, N, K, nthreads=cpu_threads())
+    Y = _empty((M, N), torch.float32)
+    ops.linear_int4(Y, f16_dev(Xb), to_dev(W), f16_dev(S), None, M, N, K)
+    y = to_np(Y)
+    print("max err", np.abs(y - ref).max(), "bound", 1e-4 * max(1.0, np.abs(ref).max()), "rel_l2", kat.rel_l2(y, ref))
+    _check_f32(y, ref)
 
 
 def test_small_batch_lm_head_ties_lowest_index():
