@@ -333,6 +333,26 @@ def test_cfg1_fused_gate_up_swiglu():
     print(check_f16_tol(to_np(Y), ref))
 
 
+@pytest.mark.parametrize("N,K", [(17406, 5120), (16386, 5120), (8194, 4096), (16384, 6144), (12290, 6144)])
+def test_pair_swiglu_leftover_split(N, K):
+    """M = 1 gate/up SwiGLU on the row-pair kernel when the pairs do not
+    divide over the waves: the leftover pairs' gate and up halves go to two
+    waves of one block and meet in LDS (an odd leftover count, a single
+    leftover pair, none); every output against the oracle."""
+    import torch
+    ops = _ops()
+    M = 1
+    Wall = synth.packed_weights(N, 2 * N, K)
+    Sall = synth.scales(N, 2 * N, K)
+    Xb = synth.activations(N, M, K)
+    dW, dS = to_dev(Wall), f16_dev(Sall)
+    Y = _empty((M, N), torch.float16)
+    ops.mlp_gate_up_swiglu_int4(Y, f16_dev(Xb), dW[:N], dS[:N], dW[N:], dS[N:], M, N, K)
+    ref = oracle.swiglu_int4(oracle.f16_to_f32(Xb), Wall[:N], Sall[:N], Wall[N:], Sall[N:],
+                             M, N, K, nthreads=cpu_threads())
+    print(check_f16_tol(to_np(Y), ref))
+
+
 @pytest.mark.parametrize("M", [1, 8])
 def test_cfg3_lm_head_argmax(M):
     import torch

@@ -70,6 +70,10 @@ struct PairParams {
     int32_t G;          // = gridDim.x times owners per block (gridDim is an argument load of its own)
     const float* norm_w; // M = 1 kernel: RMSNorm weight [K] applied to X while staging, or null
     float norm_eps;
+    // SwiGLU, strided, 0 < wr <= 2 blocks: every wave takes wq gate and wq
+    // up pairs, and leftover pair wq G + e goes to block e / 2, its gate rows
+    // to wave 2 (e % 2) and its up rows to wave 2 (e % 2) + 1
+    int32_t xsplit;
 };
 
 // The kernel arguments used before and in the streaming loop, read
@@ -92,6 +96,7 @@ struct PairArgs {
     uint64_t wm;
     int32_t G;
     const float* norm_w;
+    bool xsplit;
 };
 __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
     PairArgs a;
@@ -112,9 +117,11 @@ __device__ __forceinline__ PairArgs pair_args(const PairParams& p) {
     a.wm = p.wm;
     a.G = p.G;
     a.norm_w = p.norm_w;
+    const int xsp = p.xsplit;
     asm volatile("" ::"s"(a.X), "s"(a.w0), "s"(a.w1), "s"(a.w2), "s"(a.w3), "s"(a.s0), "s"(a.s1), "s"(a.s2),
                  "s"(a.s3), "s"(nd), "s"(r1), "s"(r2), "s"(r3), "s"(st), "s"(a.wq), "s"(a.wr), "s"(a.ws),
-                 "s"(a.wm), "s"(a.G), "s"(a.norm_w));
+                 "s"(a.wm), "s"(a.G), "s"(a.norm_w), "s"(xsp));
+    a.xsplit = xsp != 0;
     a.pb1 = nd > 1 ? r1 : 0x7FFFFFFF;
     a.pb2 = nd > 2 ? r2 : 0x7FFFFFFF;
     a.pb3 = nd > 3 ? r3 : 0x7FFFFFFF;
@@ -194,6 +201,15 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
     const int qs = strided ? nwaves : 1;
     int q0, nh;  // nh = pairs of the wave (per matrix for SwiGLU)
     pair_range(a, (uint32_t)gw, q0, nh);
+    // leftover split (SwiGLU): nh = wq for every wave, plus one item of the
+    // block's leftover pairs: pair px of matrix wave % 2
+    int has_x = 0, px = 0;
+    if (SWIGLU && a.xsplit) {
+        nh = a.wq;
+        const int e = 2 * (int)blockIdx.x + (wave >> 1);
+        has_x = e < a.wr ? 1 : 0;
+        px = a.wq * a.G + e;
+    }
     const int q1 = q0 + nh;  // contiguous ranges: one past the last pair
 
     f16x2 xp[P][16];  // the chunks' activations in the decode's pair order
@@ -217,7 +233,7 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
         u32x4 w[P];
         uint32_t s[P];
     };
-    const int nitems = SWIGLU ? 2 * nh : nh;
+    const int nitems = SWIGLU ? 2 * nh + has_x : nh;
     // a wave without pairs issues its prefetch against empty resources
     const int live = nitems > 0 ? 1 : 0;
     int lit = 0;  // load cursor (item index within the wave)
@@ -226,8 +242,13 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
         ++lit;
         int di, qq;  // descriptor, pair within it
         if (SWIGLU) {
-            di = it >= nh ? 1 : 0;
-            qq = live ? q0 + (it - di * nh) * qs : 0;
+            if (it >= 2 * nh) {  // the leftover item
+                di = wave & 1;
+                qq = px;
+            } else {
+                di = it >= nh ? 1 : 0;
+                qq = live ? q0 + (it - di * nh) * qs : 0;
+            }
         } else {
             const int q = live ? q0 + it * qs : 0;
             di = (q >= pb1) + (q >= pb2) + (q >= pb3);
@@ -376,6 +397,15 @@ __global__ __launch_bounds__(256) void gemv_pair_int4_kernel(const PairParams p)
         for (int i = lane; i < 2 * nh; i += 64) {
             const float g = res[wave][i], u = res[wave][2 * nh + i];
             reinterpret_cast<OutT*>(p.d[0].Y)[2 * (q0 + (i >> 1) * qs) + (i & 1)] = (OutT)(g / (1.0f + expf(-g)) * u);
+        }
+        // the leftover pairs: the up wave's two sums through LDS (the
+        // condition is uniform over the block: every wave reaches the barrier)
+        if (a.xsplit && 2 * (int)blockIdx.x < a.wr) {
+            __syncthreads();
+            if ((wave & 1) == 0 && has_x && lane < 2) {
+                const float g = res[wave][4 * nh + lane], u = res[wave + 1][4 * nh + lane];
+                reinterpret_cast<OutT*>(p.d[0].Y)[2 * px + lane] = (OutT)(g / (1.0f + expf(-g)) * u);
+            }
         }
         return;
     }
@@ -862,6 +892,13 @@ int pair_swiglu(hipStream_t st, void* Y, const void* X, const uint8_t* Wg, const
     const int64_t need = (p.npairs + 4LL * (kPairMaxPerWave / 2) - 1) / (4LL * (kPairMaxPerWave / 2));
     if (blocks < need) blocks = need;
     if (blocks > 65535 || !pair_split(p, 4 * blocks)) return 1;
+    // leftover pairs split by matrix over the blocks' waves: every wave then
+    // streams the same number of items (XINFER_PAIR_XSPLIT=0: off)
+    static const int xsplit_env = [] {
+        const char* v = getenv("XINFER_PAIR_XSPLIT");
+        return (v && *v) ? atoi(v) : 1;
+    }();
+    p.xsplit = (xsplit_env != 0 && p.strided && p.wr > 0 && p.wr <= 2 * blocks) ? 1 : 0;
     hipLaunchKernelGGL(k, dim3((unsigned)blocks), dim3(256), 0, st, p);
     *rc = launch_status();
     return 0;
