@@ -96,16 +96,26 @@ constexpr uint32_t kOutOfRange = 0xFFFFF000u;  // >= every buffer resource size 
 #ifndef XHIP_MB_AUX
 #define XHIP_MB_AUX 0
 #endif
-constexpr int kGP = XHIP_MB_GP;  // 128-k groups per item
+constexpr int kGP = XHIP_MB_GP;  // 128-k groups per item (the plain and SwiGLU forms)
 // Cache-policy bit for device-scope coherence (sc1): stores write through and
 // loads do not hit stale lines of another XCD's L2.
 constexpr int kDeviceCoherent = 16;
 
 static_assert(kGP == 2, "an item's two group scales are one dword");
-template <int E>
+// The LM head's items: 4 groups (16 rows x 256 bytes, its scales one
+// 2-byte load per group), 3 in flight: M = 8, N = 151936 84.8 -> 83.8 us
+// (five interleaved runs) against 2 groups and 4 in flight; 4 groups with
+// 2 or 4 in flight measured between the two.
+#ifndef XHIP_MB_GPA
+#define XHIP_MB_GPA 4
+#endif
+#ifndef XHIP_MB_PFA
+#define XHIP_MB_PFA 3
+#endif
+template <int E, int GP = kGP>
 struct MbItem {
-    u32x4 w[E * kGP];
-    uint32_t s[E * kGP];  // fp16 group scales: s[x] holds both of matrix x's (the LM head: one per s[gi])
+    u32x4 w[E * GP];
+    uint32_t s[E * GP];  // fp16 group scales: s[x] holds both of matrix x's (the LM head: one per s[gi])
     uint32_t sh[E];       // s[x]'s first scale at bit sh[x] (0, or 16 for the array's last scale)
 };
 
@@ -119,6 +129,7 @@ __device__ __forceinline__ f16x8 pack_q8(const f16x2 q[4]) {
 template <int MR, int EPI, typename OutT, int NW, int NORM = 0>
 __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p) {
     constexpr int E = (EPI == MB_SWIGLU) ? 2 : 1;  // sums per output (weight tiles per item)
+    constexpr int GP = EPI == MB_ARGMAX ? XHIP_MB_GPA : kGP;  // groups per item
     constexpr int NT = 64 * NW;
 
     extern __shared__ __align__(16) unsigned char smem[];
@@ -188,7 +199,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     const int t1 = ((wr + 1) * tiles_here) / nr;
     const int gb = (kp * ngs) >> lkw;                   // first group of this wave
     const int ngw = (((kp + 1) * ngs) >> lkw) - gb;     // groups of this wave (>= 1)
-    const int nig = (ngw + kGP - 1) / kGP;  // items per tile
+    const int nig = (ngw + GP - 1) / GP;  // items per tile
     const int nreal = (t1 - t0) * nig;
 
     const int nrec_w = (int)((uint32_t)N * row_bytes);
@@ -224,12 +235,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // the item's two group scales; sh = 16 where the dword was read 2 bytes
     // lower (its upper half is the first group's scale)
     auto load_scales = [&](const __amdgpu_buffer_rsrc_t& rs, uint32_t vs, uint32_t& sh) -> uint32_t {
-        const uint32_t o = vs + (uint32_t)(lg * (2 * kGP));
+        const uint32_t o = vs + (uint32_t)(lg * (2 * GP));
         const uint32_t oc = o < slast ? o : slast;
         sh = (o - oc) << 3;
         return __builtin_amdgcn_raw_buffer_load_b32(rs, (int)oc, 0, 0);
     };
-    auto load_next = [&](MbItem<E>& b) {
+    auto load_next = [&](MbItem<E, GP>& b) {
         // argmax: past the wave's last item, out-of-range offsets (zeros
         // without memory traffic, nothing for the epilogue's waits to wait
         // on; the other epilogues measured faster repeating the last item)
@@ -244,20 +255,20 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 #pragma unroll
             for (int e = 0; e < E; ++e) {
 #pragma unroll
-                for (int gi = 0; gi < kGP; ++gi) {
-                    const int g = __builtin_amdgcn_readfirstlane(min(lg * kGP + gi, ngw - 1));  // wave-uniform: a scalar offset
-                    b.w[e * kGP + gi] =
+                for (int gi = 0; gi < GP; ++gi) {
+                    const int g = __builtin_amdgcn_readfirstlane(min(lg * GP + gi, ngw - 1));  // wave-uniform: a scalar offset
+                    b.w[e * GP + gi] =
                         __builtin_amdgcn_raw_buffer_load_b128(e ? rw1 : rw0, (int)vw, g * 64, XHIP_MB_AUX);
                 }
                 b.s[e] = load_scales(e ? rs1 : rs0, vs, b.sh[e]);
             }
         } else {
 #pragma unroll
-            for (int gi = 0; gi < kGP; ++gi) {
+            for (int gi = 0; gi < GP; ++gi) {
                 // wave-uniform (a scalar offset; without the explicit form
                 // the compiler waterfalled some plain instantiations)
-                const int g = EPI == MB_ARGMAX ? min(lg * kGP + gi, ngw - 1)
-                                               : __builtin_amdgcn_readfirstlane(min(lg * kGP + gi, ngw - 1));
+                const int g = EPI == MB_ARGMAX ? min(lg * GP + gi, ngw - 1)
+                                               : __builtin_amdgcn_readfirstlane(min(lg * GP + gi, ngw - 1));
                 b.w[gi] = __builtin_amdgcn_raw_buffer_load_b128(rw0, (int)vw, g * 64, XHIP_MB_AUX);
                 if constexpr (EPI == MB_ARGMAX)  // the LM head measured faster with a 2-byte load per group
                     b.s[gi] = __builtin_amdgcn_raw_buffer_load_b16(rs0, (int)vs, g * 2, 0);
@@ -383,11 +394,11 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 
     // items in flight per wave: a SwiGLU item carries both matrices' groups
     // (twice the bytes), and one item less measured faster there (gate/up
-    // M = 4 / 8 28.9 / 31.4 -> 28.2 / 30.3 us) while the plain and argmax
-    // forms lost 1.5-4.6 % with it; the LM head (186 items a wave) gains
-    // from one more (M = 8 84.5 -> 83.3 us; the plain form lost with it)
-    constexpr int PF = EPI == MB_SWIGLU ? XHIP_MB_PF - 1 : EPI == MB_ARGMAX ? XHIP_MB_PF + 1 : XHIP_MB_PF;
-    MbItem<E> buf[PF + 1];
+    // M = 4 / 8 28.9 / 31.4 -> 28.2 / 30.3 us) while the plain form lost
+    // 1.5-4.6 % with it, and also with one more; the LM head's 4-group
+    // items: XHIP_MB_PFA
+    constexpr int PF = EPI == MB_SWIGLU ? XHIP_MB_PF - 1 : EPI == MB_ARGMAX ? XHIP_MB_PFA : XHIP_MB_PF;
+    MbItem<E, GP> buf[PF + 1];
 #pragma unroll
     for (int j = 0; j < PF; ++j) load_next(buf[j]);
 
@@ -502,12 +513,12 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
     // is the compile-time MR, so the four dwords of a group are immediate
     // offsets from one address.
     const f16x8* xl = xs + xslot(kq * 4, l16 < M ? l16 : M - 1);
-    auto compute_item = [&](int it, const MbItem<E>& b) {
-        f16x8 xa[kGP][4];
-        int gl[kGP];
+    auto compute_item = [&](int it, const MbItem<E, GP>& b) {
+        f16x8 xa[GP][4];
+        int gl[GP];
 #pragma unroll
-        for (int gi = 0; gi < kGP; ++gi) {
-            gl[gi] = it * kGP + gi;
+        for (int gi = 0; gi < GP; ++gi) {
+            gl[gi] = it * GP + gi;
             const f16x8* xg = xl + (gb + min(gl[gi], ngw - 1)) * (16 * MR);
 #pragma unroll
             for (int t = 0; t < 4; ++t) xa[gi][t] = xg[t * MR];
@@ -515,14 +526,14 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
 #pragma unroll
         for (int x = 0; x < E; ++x) {
             // the groups' MFMA chains are independent: interleaved
-            f32x4 c[kGP];
+            f32x4 c[GP];
 #pragma unroll
-            for (int gi = 0; gi < kGP; ++gi) c[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+            for (int gi = 0; gi < GP; ++gi) c[gi] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
 #pragma unroll
-                for (int gi = 0; gi < kGP; ++gi) {
-                    const u32x4 wv = b.w[x * kGP + gi];
+                for (int gi = 0; gi < GP; ++gi) {
+                    const u32x4 wv = b.w[x * GP + gi];
                     const uint32_t wd = t == 0 ? wv.x : t == 1 ? wv.y : t == 2 ? wv.z : wv.w;
                     f16x2 q[4];
                     dequant8(wd, q);
@@ -530,7 +541,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mb_int4_kernel(const MbParams p)
                 }
             }
 #pragma unroll
-            for (int gi = 0; gi < kGP; ++gi) {
+            for (int gi = 0; gi < GP; ++gi) {
                 const uint16_t sb = EPI == MB_ARGMAX ? (uint16_t)b.s[gi] : (uint16_t)((b.s[x] >> b.sh[x]) >> (16 * gi));
                 const float s = gl[gi] < ngw ? h2f(sb) : 0.0f;
 #pragma unroll
