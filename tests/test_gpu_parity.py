@@ -266,6 +266,54 @@ def test_pair_kernel_bias_residual_descs():
         print(check_f16_tol(to_np(Y), ref))
 
 
+@pytest.mark.parametrize("N,K", [(8194, 5120), (9000, 4096), (12290, 6144), (10000, 5120)])
+def test_pair_plain_leftover_rows(N, K):
+    """M = 1 plain launches on the row-pair kernel whose pairs do not divide
+    over the waves (one leftover pair, 404, 904 of them): fp16 plain, fp32
+    with bias, fp16 residual; every output against the oracle."""
+    import torch
+    ops = _ops()
+    W, S = synth.packed_weights(N, N, K), synth.scales(N, N, K)
+    Xb = synth.activations(N, 1, K)
+    X = oracle.f16_to_f32(Xb)
+    bias = kat.uniform_x(N + 1, 1, N, -1, 1)[0]
+    dX, dW, dS = f16_dev(Xb), to_dev(W), f16_dev(S)
+    ref = oracle.linear_int4(X, W, S, 1, N, K, nthreads=cpu_threads())
+    Y = _empty((1, N), torch.float16)
+    ops.linear_int4(Y, dX, dW, dS, None, 1, N, K)
+    print(check_f16_tol(to_np(Y), ref))
+    Yf = _empty((1, N), torch.float32)
+    ops.linear_int4(Yf, dX, dW, dS, to_dev(bias), 1, N, K)
+    reff = oracle.linear_int4(X, W, S, 1, N, K, bias=bias, nthreads=cpu_threads())
+    yf = to_np(Yf)
+    assert np.abs(yf - reff).max() <= 1e-4 * max(1.0, np.abs(reff).max()) and kat.rel_l2(yf, reff) <= 1e-4
+    r0 = synth.activations(N + 2, 1, N)
+    R = f16_dev(r0)
+    ops.linear_int4_residual(R, dX, dW, dS, None, 1, N, K)
+    print(check_f16_tol(to_np(R), oracle.f16_to_f32(r0).astype(np.float64) + ref))
+
+
+def test_pair_plain_leftover_rows_la_in_proj():
+    """The fused LA in_proj (10240 + 6144 + 48 + 48 rows, 8240 pairs over
+    1024 waves: 48 leftover pairs) on the row-pair kernel, every output
+    against the oracle."""
+    import torch
+    ops = _ops()
+    K = 5120
+    Xb = synth.activations(5, 1, K)
+    X = oracle.f16_to_f32(Xb)
+    descs, outs, refs = [], [], []
+    for p, Np in enumerate((10240, 6144, 48, 48)):
+        Wp, Sp = synth.packed_weights(50 + p, Np, K), synth.scales(50 + p, Np, K)
+        refs.append(oracle.linear_int4(X, Wp, Sp, 1, Np, K, nthreads=cpu_threads()))
+        Y = _empty((1, Np), torch.float16)
+        outs.append(Y)
+        descs.append(ops.FusedProjectionDesc(Y, to_dev(Wp), f16_dev(Sp), None, Np))
+    ops.linear_int4_fused(f16_dev(Xb), descs, 4, 1, K)
+    for Y, ref in zip(outs, refs):
+        print(check_f16_tol(to_np(Y), ref))
+
+
 @pytest.mark.parametrize("N,K", [(4096, 8192), (6144, 24576), (4100, 7168), (5120, 17408)])
 def test_pair_kernel_long_k(N, K):
     """M = 1 beyond K = 6144: a row pair's 1 KB pieces split over four
