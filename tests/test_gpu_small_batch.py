@@ -165,13 +165,13 @@ def test_small_batch_lm_head_argmax(M):
 
 
 @pytest.mark.parametrize("M,N,K", [(3, 1001, 640), (8, 4099, 1152), (5, 33, 384), (2, 17, 128),
-                                   (4, 3001, 17408), (8, 1000, 9216)])
+                                   (4, 3001, 17408), (8, 1000, 9216), (8, 2003, 17408)])
 def test_small_batch_lm_head_odd_groups_ragged_rows(M, N, K):
     """LM head with odd group counts (a wave's last item has a padding
     group) and N not a multiple of 16 (the last tile's rows clamped), the
-    winner planted in the last row: every logit and every id.  The last two
-    shapes stage X in two rounds (the biased decode's bias terms summed in
-    both)."""
+    winner planted in the last row: every logit and every id.  K = 17408 at
+    M = 4 and K = 9216 at M = 8 stage X in two rounds; at M = 8, K = 17408
+    the X slice exceeds LDS and the call takes the per-row path."""
     import torch
     ops = _ops()
     W, S, Xb = _inputs(60 + M, M, N, K, 0.01)
